@@ -1,0 +1,165 @@
+/*
+ * ltx_block.h — C ABI of the MI355X-native LTX-2.5 DiT block forward.
+ *
+ * Drop-in for the one hot path the reference builds with ZML/XLA: the int8
+ * block QBlock.qBlockOutAll (ltx/block.zig:544-574) and its f32 twin
+ * Block.wBlockOut (ltx/block.zig:351-353), the packed int8-g128 blob format
+ * (tools/pack_block.py, tools/quantize_block.py) and the streaming loader
+ * (ltx/loader.zig).
+ *
+ * Conventions follow the reference's only C ABI (coli-zml/coli/abi.zig:1-10):
+ *   - every entry point returns an int status, NON-ZERO = success (LTX_OK);
+ *   - C++ exceptions never cross this boundary;
+ *   - objects are opaque handles; error text via ltx_last_error();
+ *   - fault injection: environment LTX_FAIL_AFTER=N makes the N-th checked
+ *     HIP runtime call of the process fail, so every HIP-error path can be
+ *     driven from the host.
+ * All tensors are device pointers owned by the caller unless stated; calls
+ * are asynchronous on the given stream (NULL = the null stream). A context is
+ * not thread-safe (one consumer thread, as in ltx/e2e_prod.zig:382-399).
+ */
+#ifndef LTX_BLOCK_H
+#define LTX_BLOCK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LTX_OK 1
+#define LTX_FAIL 0
+
+/* Model geometry (ltx/block.zig:14-18). */
+#define LTX_DIM 4096
+#define LTX_HEADS 32
+#define LTX_HEAD_DIM 128
+#define LTX_FF_DIM 16384
+
+/* Arithmetic modes. F16/BF16: 16-bit MFMA operands, f32 accumulation, f32
+ * residual stream, norms, AdaLN values and softmax statistics. F32: f32
+ * everywhere (the reference graph's own precision). */
+enum { LTX_MODE_F16 = 0, LTX_MODE_BF16 = 1, LTX_MODE_F32 = 2 };
+
+typedef struct ltx_ctx ltx_ctx;
+typedef struct ltx_block_weights ltx_block_weights;
+
+/* Base weight tensors in WEIGHT_SPECS order (ltx/block.zig:377-406): bf16
+ * except sst [9][4096] and psst [2][4096] (f32). */
+enum {
+    LTX_W_Q1_W, LTX_W_Q1_B, LTX_W_K1_W, LTX_W_K1_B, LTX_W_V1_W, LTX_W_V1_B, LTX_W_O1_W, LTX_W_O1_B,
+    LTX_W_QN1, LTX_W_KN1, LTX_W_G1_W, LTX_W_G1_B, LTX_W_Q2_W, LTX_W_Q2_B, LTX_W_K2_W, LTX_W_K2_B,
+    LTX_W_V2_W, LTX_W_V2_B, LTX_W_O2_W, LTX_W_O2_B, LTX_W_QN2, LTX_W_KN2, LTX_W_G2_W, LTX_W_G2_B,
+    LTX_W_FF1_W, LTX_W_FF2_W, LTX_W_SST, LTX_W_PSST, LTX_W_COUNT
+};
+
+/* int8 companions in Q8_SPECS order (ltx/loader.zig:147-156), plus the two
+ * output projections (tools/quantize_block.py:23, class "out"). */
+enum { LTX_Q_Q1, LTX_Q_K1, LTX_Q_V1, LTX_Q_Q2, LTX_Q_K2, LTX_Q_V2, LTX_Q_F1, LTX_Q_F2, LTX_Q_O1, LTX_Q_O2, LTX_Q_COUNT };
+
+/* ---- context ----------------------------------------------------------- */
+
+/* Select `device`, load the gfx950 code objects (hipModuleLoadData), create
+ * the context. Replaces zml.Platform.auto + platform.compile
+ * (ltx/e2e_prod.zig:187-189, 297-299). */
+int ltx_init(int device, ltx_ctx** out);
+void ltx_destroy(ltx_ctx* ctx);
+/* Last error of `ctx`, or of the calling thread when ctx is NULL. */
+const char* ltx_last_error(const ltx_ctx* ctx);
+/* Library / code-object build identification. */
+const char* ltx_version(void);
+
+/* ---- weights ----------------------------------------------------------- */
+
+/* Upload one block from a blob image laid out per its manifest
+ * (ltx/loader.zig:133-172, buildBlockBufs + buildQuantBufs): entries are
+ * found by normalised name "transformer_blocks_{i}_{stem}[_q8|_q8scale]"
+ * (ltx/loader.zig:100-129). `mem` is the blob bytes (an mmap or a ring slot),
+ * `manifest_json` the text of blob_manifest.json. q8scale entries may be F32
+ * (the reference format) or F16. Missing q8 entries fall back to the bf16
+ * base weight for that projection. */
+int ltx_block_weights_from_blob(ltx_ctx* ctx, const void* mem, uint64_t mem_bytes, const char* manifest_json,
+                                int64_t block_idx, ltx_block_weights** out);
+
+/* Upload one block from host pointers: base[LTX_W_COUNT] (bf16 bits / f32),
+ * q8[LTX_Q_COUNT] int8 [O][I] or NULL, q8s[LTX_Q_COUNT] scales [O][I/128]
+ * (f32, or f16 when scale_f16). */
+int ltx_block_weights_from_host(ltx_ctx* ctx, const void* const* base, const int8_t* const* q8,
+                                const void* const* q8s, int scale_f16, ltx_block_weights** out);
+void ltx_block_weights_free(ltx_ctx* ctx, ltx_block_weights* w);
+/* Device bytes held by one uploaded block. */
+uint64_t ltx_block_weights_bytes(const ltx_block_weights* w);
+
+/* ---- the block forward ------------------------------------------------- */
+
+/* y = QBlock.qBlockOutAll(x, tstab, tidx, ctx, pts2, cos, sin)
+ * (ltx/block.zig:544-574), self-attention blockwise (ltx/block.zig:105-154).
+ *   x      [T][4096] f32         tstab [K][9][4096] f32   tidx [T] i32
+ *   ctx_tokens [S][4096] f32     pts2  [2][4096] f32
+ *   cos, sin [T][32][64] f32 (graph layout, ltx/block_conformance.zig:255-267)
+ *   y      [T][4096] f32 (may not alias x)
+ * Argument order follows the reference method (ltx/e2e_prod.zig:238-247). */
+int ltx_block_forward(ltx_ctx* ctx, const ltx_block_weights* w, const float* x, const float* tstab, int K,
+                      const int32_t* tidx, const float* ctx_tokens, int S, const float* pts2, const float* cos,
+                      const float* sin, int T, float* y, int mode, void* stream);
+
+/* Intermediate tensors of the last forward, for staged parity checks
+ * (the staged methods of ltx/block.zig:248-338). Device pointer + bytes,
+ * valid until the next forward on this context. */
+enum {
+    LTX_ST_NORM_MSA,    /* s1NormMsa: modulated norm, operand dtype [T][4096] */
+    LTX_ST_Q1,          /* normed+roped q, head-major [32][T][128] (f32 mode: [T][4096]) */
+    LTX_ST_K1,          /* normed+roped k, same layout */
+    LTX_ST_V1,          /* v: [32][128][T] (f32 mode: [T][4096]) */
+    LTX_ST_GLOG1,       /* gate logits [T][32] f32 */
+    LTX_ST_ATTN1,       /* gated merged attention before out-proj [T][4096] */
+    LTX_ST_X_SA,        /* s4AfterSa [T][4096] f32 */
+    LTX_ST_ATTN_IN,     /* cross-attention query input [T][4096] */
+    LTX_ST_ATTN2,       /* gated merged cross-attention [T][4096] */
+    LTX_ST_X_CA,        /* x after cross-attention [T][4096] f32 */
+    LTX_ST_FF_IN,       /* s6FfIn [T][4096] */
+    LTX_ST_FF_H,        /* gelu(ff1) [T][16384] */
+    LTX_ST_COUNT
+};
+int ltx_block_stage(ltx_ctx* ctx, int stage, void** dev_ptr, uint64_t* bytes);
+
+/* ---- isolated operators (the microbenchmark surface, ltx/smoke.zig) ---- */
+
+/* y[M][N] = a[M][K] . dq4(q, s)^T (+ bias) with optional GELU-tanh.
+ * a: 16-bit [M][K] (mode F16/BF16) or f32 (mode F32); q int8 [N][K];
+ * scales [N][K/128] f32 or f16; y f32 (out_f32) or 16-bit. Mirrors linQ
+ * (ltx/block.zig:473-477). */
+int ltx_op_linear_q8(ltx_ctx* ctx, const void* a, const int8_t* q, const void* scales, int scale_f16,
+                     const float* bias, void* y, int out_f32, int M, int N, int K, int gelu, int mode,
+                     void* stream);
+
+/* Attention with per-(token, head) gate (gate logits glog [Lq][32] f32, or
+ * NULL for no gate). F16/BF16: q, k [32][L][128] 16-bit, vt [32][128][Lkv]
+ * 16-bit, out [Lq][4096] 16-bit. F32: q, k, v, out [L][4096] f32. */
+int ltx_op_attention(ltx_ctx* ctx, const void* q, const void* k, const void* v, const float* glog, void* out,
+                     int lq, int lkv, int mode, void* stream);
+
+/* Dequantisation probe: out32 = f32(q) * s (bit-exact dq4, ltx/block.zig:
+ * 462-471) and out16 = that value rounded to the mode's operand type. */
+int ltx_op_dequant(ltx_ctx* ctx, const int8_t* q, const void* scales, int scale_f16, int N, int K, float* out32,
+                   void* out16, int mode, void* stream);
+
+/* ---- host utilities ---------------------------------------------------- */
+
+/* 3D RoPE tables, host f64 (ltx/block_conformance.zig:87-126). grid
+ * [3][T][2] f32 (start, end); outputs f32 in the bundle layout [32][T][64]
+ * when graph_layout == 0, or the graph layout [T][32][64] when 1. */
+int ltx_rope_tables(const float* grid, int T, float* cos_out, float* sin_out, int graph_layout);
+
+/* Per-kernel timing with HIP events on the launch stream. */
+int ltx_profile_enable(ltx_ctx* ctx, int enable);
+/* Total milliseconds and launch count of kernels whose name contains
+ * `substr` (all recorded launches when substr is NULL or empty). Synchronises. */
+int ltx_profile_read(ltx_ctx* ctx, const char* substr, double* total_ms, int* count);
+int ltx_profile_reset(ltx_ctx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

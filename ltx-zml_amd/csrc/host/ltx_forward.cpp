@@ -1,0 +1,428 @@
+// Block forward orchestration: QBlock.qBlockOutAll (ltx/block.zig:544-574)
+// as a sequence of gfx950 kernel launches on one stream, plus the isolated
+// operator entry points.
+#include <cmath>
+#include <cstring>
+
+#include "ltx_internal.hpp"
+
+namespace ltx {
+
+static const char* msuffix(int mode) { return mode == LTX_MODE_BF16 ? "bf16" : "f16"; }
+
+static size_t al(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Bump allocator over the context workspace.
+struct Carve {
+    char* base;
+    size_t off = 0;
+    size_t total = 0;
+    bool dry;
+    void* take(size_t n) {
+        void* p = dry ? nullptr : base + off;
+        off += al(n);
+        return p;
+    }
+};
+
+struct Ws16 {
+    void *n_msa, *qk32, *vt1, *qh1, *kh1, *glog1, *o1, *x_sa, *attn_in, *q2_32, *glog2, *enc, *k2_32, *vt2, *qh2,
+        *kh2, *o2, *x_ca, *ff_in, *h;
+};
+
+static void carve16(Carve& c, Ws16& w, size_t T, size_t S) {
+    const size_t D = LTX_D;
+    w.n_msa = c.take(T * D * 2);
+    w.qk32 = c.take(T * 2 * D * 4);
+    w.vt1 = c.take(T * D * 2);
+    w.qh1 = c.take(T * D * 2);
+    w.kh1 = c.take(T * D * 2);
+    w.glog1 = c.take(T * LTX_H * 4);
+    w.o1 = c.take(T * D * 2);
+    w.x_sa = c.take(T * D * 4);
+    w.attn_in = c.take(T * D * 2);
+    w.q2_32 = c.take(T * D * 4);
+    w.glog2 = c.take(T * LTX_H * 4);
+    w.enc = c.take(S * D * 2);
+    w.k2_32 = c.take(S * D * 4);
+    w.vt2 = c.take(S * D * 2);
+    w.qh2 = c.take(T * D * 2);
+    w.kh2 = c.take(S * D * 2);
+    w.o2 = c.take(T * D * 2);
+    w.x_ca = c.take(T * D * 4);
+    w.ff_in = c.take(T * D * 2);
+    w.h = c.take(T * LTX_FF * 2);
+}
+
+struct Ws32 {
+    void *n_msa, *q, *k, *v, *glog1, *o1, *x_sa, *attn_in, *q2, *enc, *k2, *v2, *glog2, *o2, *x_ca, *ff_in, *h;
+};
+
+static void carve32(Carve& c, Ws32& w, size_t T, size_t S) {
+    const size_t D = LTX_D;
+    w.n_msa = c.take(T * D * 4);
+    w.q = c.take(T * D * 4);
+    w.k = c.take(T * D * 4);
+    w.v = c.take(T * D * 4);
+    w.glog1 = c.take(T * LTX_H * 4);
+    w.o1 = c.take(T * D * 4);
+    w.x_sa = c.take(T * D * 4);
+    w.attn_in = c.take(T * D * 4);
+    w.q2 = c.take(T * D * 4);
+    w.enc = c.take(S * D * 4);
+    w.k2 = c.take(S * D * 4);
+    w.v2 = c.take(S * D * 4);
+    w.glog2 = c.take(T * LTX_H * 4);
+    w.o2 = c.take(T * D * 4);
+    w.x_ca = c.take(T * D * 4);
+    w.ff_in = c.take(T * D * 4);
+    w.h = c.take(T * LTX_FF * 4);
+}
+
+static void ensure_ws(ltx_ctx* c, size_t T, size_t S, int mode) {
+    Carve cv{nullptr, 0, 0, true};
+    if (mode == LTX_MODE_F32) {
+        Ws32 w;
+        carve32(cv, w, T, S);
+    } else {
+        Ws16 w;
+        carve16(cv, w, T, S);
+    }
+    if (c->ws.bytes < cv.off) {
+        HIPC(hipDeviceSynchronize());
+        c->ws.alloc(cv.off);
+    }
+}
+
+// ---- launch helpers -------------------------------------------------------
+
+static LtxAda make_ada(const ltx_block_weights* w, const float* tstab, const int32_t* tidx) {
+    LtxAda a;
+    a.sst = (const float*)w->sst.p;
+    a.tstab = tstab;
+    a.tidx = tidx;
+    return a;
+}
+
+static void norm_mod(ltx_ctx* c, int mode, const float* x, void* y, LtxAda ada, int rows, int ish, int isc,
+                     hipStream_t st) {
+    LtxNormArgs a{x, y, ada, rows, ish, isc};
+    const char* k = mode == LTX_MODE_F32 ? "ltx_norm_mod_f32" : mode == LTX_MODE_BF16 ? "ltx_norm_mod_bf16" : "ltx_norm_mod_f16";
+    c->launch(k, rows, 1, 1, 256, &a, st);
+}
+
+// 16-bit GEMM: y = A . W^T with the given epilogue.
+static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M, int lda, int epi, LtxGemmArgs g,
+                   hipStream_t st, const char* label = nullptr) {
+    if (p.N % 256 != 0 || p.K % 64 != 0) throw Error("gemm16: N must be a multiple of 256 and K of 64");
+    g.a = A;
+    g.M = M;
+    g.N = p.N;
+    g.K = p.K;
+    g.lda = lda;
+    g.bias = (const float*)p.bias.p;
+    const char* bk;
+    if (p.q8) {
+        g.b = p.q.p;
+        g.scales = p.s.p;
+        bk = p.scale_f16 ? "i8f16" : "i8f32";
+    } else {
+        g.b = mode == LTX_MODE_BF16 ? p.w_bf16.p : p.w_f16.p;
+        g.scales = nullptr;
+        bk = "w16";
+        if (epi == LTX_EPI_QKV) throw Error("gemm16: the QKV epilogue needs int8 weights");
+    }
+    if (!g.b) throw Error("gemm16: weight not resident for this mode");
+    g.tiles_m = (M + 255) / 256;
+    g.tiles_n = p.N / 256;
+    char name[64];
+    std::snprintf(name, sizeof(name), "ltx_gemm_%s_%s_%s", msuffix(mode), bk,
+                  epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv");
+    c->launch(name, g.tiles_m * g.tiles_n, 1, 1, 256, &g, st, label);
+}
+
+static void gate16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M, float* out, hipStream_t st) {
+    LtxGateArgs g{A, mode == LTX_MODE_BF16 ? p.w_bf16.p : p.w_f16.p, (const float*)p.bias.p, out, M};
+    c->launch(mode == LTX_MODE_BF16 ? "ltx_gate_bf16" : "ltx_gate_f16", (M + 127) / 128, 1, 1, 256, &g, st);
+}
+
+static void qknorm16(ltx_ctx* c, int mode, const float* x, int ldx, const void* w, const float* cs, const float* sn,
+                     void* y, int rows, hipStream_t st) {
+    LtxQkNormArgs a{x, (const float*)w, cs, sn, y, rows, ldx};
+    c->launch(mode == LTX_MODE_BF16 ? "ltx_qknorm_bf16" : "ltx_qknorm_f16", rows, 1, 1, 256, &a, st);
+}
+
+static void attn16(ltx_ctx* c, int mode, const void* q, const void* k, const void* vt, const float* glog, void* out,
+                   int lq, int lkv, hipStream_t st, const char* label = nullptr) {
+    LtxAttnArgs a;
+    a.q = q;
+    a.k = k;
+    a.vt = vt;
+    a.glog = glog;
+    a.out = out;
+    a.lq = lq;
+    a.lkv = lkv;
+    a.scale_log2 = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;
+    a.q_tiles = (lq + 255) / 256;
+    c->launch(mode == LTX_MODE_BF16 ? "ltx_attn_bf16" : "ltx_attn_f16", a.q_tiles * LTX_H, 1, 1, 256, &a, st, label);
+}
+
+// f32-mode GEMM over rows [r0, r0 + N) of a (possibly fused) projection.
+static void gemm32(ltx_ctx* c, const LtxProj& p, int r0, int N, const float* A, int M, float* out, int epi,
+                   const float* resid, LtxAda ada, int igate, int gelu, hipStream_t st) {
+    LtxGemm32Args g{};
+    g.a = A;
+    const size_t G = p.K / LTX_GROUP;
+    if (p.q8) {
+        g.bkind = p.scale_f16 ? 1 : 0;
+        g.b = (const int8_t*)p.q.p + (size_t)r0 * p.K;
+        g.scales = (const char*)p.s.p + (size_t)r0 * G * (p.scale_f16 ? 2 : 4);
+    } else {
+        g.bkind = 2;
+        g.b = (const uint16_t*)p.w_bf16.p + (size_t)r0 * p.K;
+    }
+    g.bias = p.bias.p ? (const float*)p.bias.p + r0 : nullptr;
+    g.out = out;
+    g.resid = resid;
+    g.ada = ada;
+    g.M = M;
+    g.N = N;
+    g.K = p.K;
+    g.epi = epi;
+    g.gelu = gelu;
+    g.igate = igate;
+    c->launch("ltx_gemm_f32", (N + 63) / 64, (M + 63) / 64, 1, 256, &g, st);
+}
+
+static void qknorm32(ltx_ctx* c, float* x, const void* w, const float* cs, const float* sn, int rows, hipStream_t st) {
+    LtxQkNorm32Args a{x, (const float*)w, cs, sn, rows, LTX_D};
+    c->launch("ltx_qknorm_f32", rows, 1, 1, 256, &a, st);
+}
+
+static void attn32(ltx_ctx* c, const float* q, const float* k, const float* v, const float* glog, float* out, int lq,
+                   int lkv, hipStream_t st) {
+    LtxAttn32Args a{q, k, v, glog, out, lq, lkv, 1.0f / std::sqrt(128.0f)};
+    c->launch("ltx_attn_f32", (lq + 63) / 64, LTX_H, 1, 64, &a, st);
+}
+
+static void set_stage(ltx_ctx* c, int id, void* p, size_t bytes) {
+    c->stage_ptr[id] = p;
+    c->stage_bytes[id] = bytes;
+}
+
+// ---- the block ------------------------------------------------------------
+
+void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const float* tstab, int K,
+                   const int32_t* tidx, const float* ctxv, int S, const float* pts2, const float* cs, const float* sn,
+                   int T, float* y, int mode, hipStream_t st) {
+    if (!w) throw Error("NULL weights");
+    if (T <= 0 || S <= 0 || K <= 0) throw Error("T, S and K must be positive");
+    if (!x || !tstab || !tidx || !ctxv || !pts2 || !cs || !sn || !y) throw Error("NULL tensor argument");
+    if ((const void*)x == (const void*)y) throw Error("y may not alias x");
+    if (mode != LTX_MODE_F16 && mode != LTX_MODE_BF16 && mode != LTX_MODE_F32) throw Error("unknown mode");
+    HIPC(hipSetDevice(c->device));
+    ensure_ws(c, (size_t)T, (size_t)S, mode);
+    std::memset(c->stage_ptr, 0, sizeof(c->stage_ptr));
+    const size_t TD = (size_t)T * LTX_D, SD = (size_t)S * LTX_D;
+    LtxAda ada = make_ada(w, tstab, tidx);
+    Carve cv{(char*)c->ws.p, 0, 0, false};
+
+    if (mode == LTX_MODE_F32) {
+        Ws32 b;
+        carve32(cv, b, T, S);
+        // self-attention (ltx/block.zig:546-547, qAttn1 520-530)
+        norm_mod(c, mode, x, b.n_msa, ada, T, 0, 1, st);
+        gemm32(c, w->qkv1, 0, LTX_D, (const float*)b.n_msa, T, (float*)b.q, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
+        gemm32(c, w->qkv1, LTX_D, LTX_D, (const float*)b.n_msa, T, (float*)b.k, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
+        gemm32(c, w->qkv1, 2 * LTX_D, LTX_D, (const float*)b.n_msa, T, (float*)b.v, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
+        gemm32(c, w->g1, 0, LTX_H, (const float*)b.n_msa, T, (float*)b.glog1, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
+        qknorm32(c, (float*)b.q, w->qn1.p, cs, sn, T, st);
+        qknorm32(c, (float*)b.k, w->kn1.p, cs, sn, T, st);
+        attn32(c, (const float*)b.q, (const float*)b.k, (const float*)b.v, (const float*)b.glog1, (float*)b.o1, T, T, st);
+        gemm32(c, w->o1, 0, LTX_D, (const float*)b.o1, T, (float*)b.x_sa, LTX_EPI_RESID_GATE, x, ada, 2, 0, st);
+        // cross-attention (ltx/block.zig:548-568)
+        norm_mod(c, mode, (const float*)b.x_sa, b.attn_in, ada, T, 6, 7, st);
+        LtxEncArgs ea{ctxv, (const float*)w->psst.p, pts2, b.enc, S};
+        c->launch("ltx_enc_f32", S, 1, 1, 256, &ea, st);
+        gemm32(c, w->q2, 0, LTX_D, (const float*)b.attn_in, T, (float*)b.q2, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
+        gemm32(c, w->kv2, 0, LTX_D, (const float*)b.enc, S, (float*)b.k2, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
+        gemm32(c, w->kv2, LTX_D, LTX_D, (const float*)b.enc, S, (float*)b.v2, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
+        gemm32(c, w->g2, 0, LTX_H, (const float*)b.attn_in, T, (float*)b.glog2, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
+        qknorm32(c, (float*)b.q2, w->qn2.p, nullptr, nullptr, T, st);
+        qknorm32(c, (float*)b.k2, w->kn2.p, nullptr, nullptr, S, st);
+        attn32(c, (const float*)b.q2, (const float*)b.k2, (const float*)b.v2, (const float*)b.glog2, (float*)b.o2, T, S, st);
+        gemm32(c, w->o2, 0, LTX_D, (const float*)b.o2, T, (float*)b.x_ca, LTX_EPI_RESID_GATE, (const float*)b.x_sa, ada, 8, 0, st);
+        // feed-forward (ltx/block.zig:569-573)
+        norm_mod(c, mode, (const float*)b.x_ca, b.ff_in, ada, T, 3, 4, st);
+        gemm32(c, w->f1, 0, LTX_FF, (const float*)b.ff_in, T, (float*)b.h, LTX_EPI_STORE, nullptr, ada, 0, 1, st);
+        gemm32(c, w->f2, 0, LTX_D, (const float*)b.h, T, y, LTX_EPI_RESID_GATE, (const float*)b.x_ca, ada, 5, 0, st);
+        set_stage(c, LTX_ST_NORM_MSA, b.n_msa, TD * 4);
+        set_stage(c, LTX_ST_Q1, b.q, TD * 4);
+        set_stage(c, LTX_ST_K1, b.k, TD * 4);
+        set_stage(c, LTX_ST_V1, b.v, TD * 4);
+        set_stage(c, LTX_ST_GLOG1, b.glog1, (size_t)T * LTX_H * 4);
+        set_stage(c, LTX_ST_ATTN1, b.o1, TD * 4);
+        set_stage(c, LTX_ST_X_SA, b.x_sa, TD * 4);
+        set_stage(c, LTX_ST_ATTN_IN, b.attn_in, TD * 4);
+        set_stage(c, LTX_ST_ATTN2, b.o2, TD * 4);
+        set_stage(c, LTX_ST_X_CA, b.x_ca, TD * 4);
+        set_stage(c, LTX_ST_FF_IN, b.ff_in, TD * 4);
+        set_stage(c, LTX_ST_FF_H, b.h, (size_t)T * LTX_FF * 4);
+        return;
+    }
+
+    if (!w->qkv1.q8 || !w->kv2.q8) throw Error("16-bit modes need int8 q/k/v weights (the QBlock recipe)");
+    Ws16 b;
+    carve16(cv, b, T, S);
+    // self-attention: n = modulate(rms(x), ada1, ada0); fused q|k|v GEMM
+    norm_mod(c, mode, x, b.n_msa, ada, T, 0, 1, st);
+    LtxGemmArgs g{};
+    g.out = b.qk32;
+    g.out2 = b.vt1;
+    g.nsplit = 2 * LTX_D;
+    gemm16(c, mode, w->qkv1, b.n_msa, T, LTX_D, LTX_EPI_QKV, g, st, "gemm:qkv1");
+    gate16(c, mode, w->g1, b.n_msa, T, (float*)b.glog1, st);
+    qknorm16(c, mode, (const float*)b.qk32, 2 * LTX_D, w->qn1.p, cs, sn, b.qh1, T, st);
+    qknorm16(c, mode, (const float*)b.qk32 + LTX_D, 2 * LTX_D, w->kn1.p, cs, sn, b.kh1, T, st);
+    attn16(c, mode, b.qh1, b.kh1, b.vt1, (const float*)b.glog1, b.o1, T, T, st, "attn:self");
+    g = LtxGemmArgs{};
+    g.out = b.x_sa;
+    g.resid = x;
+    g.ada = ada;
+    g.igate = 2;
+    g.ldo = LTX_D;
+    gemm16(c, mode, w->o1, b.o1, T, LTX_D, LTX_EPI_RESID_GATE, g, st, "gemm:o1");
+    // cross-attention
+    norm_mod(c, mode, (const float*)b.x_sa, b.attn_in, ada, T, 6, 7, st);
+    g = LtxGemmArgs{};
+    g.out = b.q2_32;
+    g.ldo = LTX_D;
+    g.out_f32 = 1;
+    gemm16(c, mode, w->q2, b.attn_in, T, LTX_D, LTX_EPI_STORE, g, st, "gemm:q2");
+    gate16(c, mode, w->g2, b.attn_in, T, (float*)b.glog2, st);
+    LtxEncArgs ea{ctxv, (const float*)w->psst.p, pts2, b.enc, S};
+    c->launch(mode == LTX_MODE_BF16 ? "ltx_enc_bf16" : "ltx_enc_f16", S, 1, 1, 256, &ea, st);
+    g = LtxGemmArgs{};
+    g.out = b.k2_32;
+    g.out2 = b.vt2;
+    g.nsplit = LTX_D;
+    gemm16(c, mode, w->kv2, b.enc, S, LTX_D, LTX_EPI_QKV, g, st, "gemm:kv2");
+    qknorm16(c, mode, (const float*)b.q2_32, LTX_D, w->qn2.p, nullptr, nullptr, b.qh2, T, st);
+    qknorm16(c, mode, (const float*)b.k2_32, LTX_D, w->kn2.p, nullptr, nullptr, b.kh2, S, st);
+    attn16(c, mode, b.qh2, b.kh2, b.vt2, (const float*)b.glog2, b.o2, T, S, st, "attn:cross");
+    g = LtxGemmArgs{};
+    g.out = b.x_ca;
+    g.resid = (const float*)b.x_sa;
+    g.ada = ada;
+    g.igate = 8;
+    g.ldo = LTX_D;
+    gemm16(c, mode, w->o2, b.o2, T, LTX_D, LTX_EPI_RESID_GATE, g, st, "gemm:o2");
+    // feed-forward
+    norm_mod(c, mode, (const float*)b.x_ca, b.ff_in, ada, T, 3, 4, st);
+    g = LtxGemmArgs{};
+    g.out = b.h;
+    g.ldo = LTX_FF;
+    g.gelu = 1;
+    gemm16(c, mode, w->f1, b.ff_in, T, LTX_D, LTX_EPI_STORE, g, st, "gemm:ff1");
+    g = LtxGemmArgs{};
+    g.out = y;
+    g.resid = (const float*)b.x_ca;
+    g.ada = ada;
+    g.igate = 5;
+    g.ldo = LTX_D;
+    gemm16(c, mode, w->f2, b.h, T, LTX_FF, LTX_EPI_RESID_GATE, g, st, "gemm:ff2");
+
+    set_stage(c, LTX_ST_NORM_MSA, b.n_msa, TD * 2);
+    set_stage(c, LTX_ST_Q1, b.qh1, TD * 2);
+    set_stage(c, LTX_ST_K1, b.kh1, TD * 2);
+    set_stage(c, LTX_ST_V1, b.vt1, TD * 2);
+    set_stage(c, LTX_ST_GLOG1, b.glog1, (size_t)T * LTX_H * 4);
+    set_stage(c, LTX_ST_ATTN1, b.o1, TD * 2);
+    set_stage(c, LTX_ST_X_SA, b.x_sa, TD * 4);
+    set_stage(c, LTX_ST_ATTN_IN, b.attn_in, TD * 2);
+    set_stage(c, LTX_ST_ATTN2, b.o2, TD * 2);
+    set_stage(c, LTX_ST_X_CA, b.x_ca, TD * 4);
+    set_stage(c, LTX_ST_FF_IN, b.ff_in, TD * 2);
+    set_stage(c, LTX_ST_FF_H, b.h, (size_t)T * LTX_FF * 2);
+    (void)SD;
+}
+
+}  // namespace ltx
+
+
+extern "C" {
+
+int ltx_block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const float* tstab, int K,
+                      const int32_t* tidx, const float* ctx_tokens, int S, const float* pts2, const float* cos,
+                      const float* sin, int T, float* y, int mode, void* stream) {
+    LTX_GUARD(c, {
+        if (!c) throw ltx::Error("NULL context");
+        ltx::block_forward(c, w, x, tstab, K, tidx, ctx_tokens, S, pts2, cos, sin, T, y, mode, (hipStream_t)stream);
+    })
+}
+
+int ltx_op_linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* scales, int scale_f16, const float* bias,
+                     void* y, int out_f32, int M, int N, int K, int gelu, int mode, void* stream) {
+    LTX_GUARD(c, {
+        if (!c) throw ltx::Error("NULL context");
+        if (M <= 0 || N <= 0 || K <= 0 || K % 128) throw ltx::Error("bad GEMM shape (K must be a multiple of 128)");
+        HIPC(hipSetDevice(c->device));
+        // Borrow the caller's buffers through a non-owning projection view.
+        LtxProj p;
+        p.N = N;
+        p.K = K;
+        p.q8 = true;
+        p.scale_f16 = scale_f16;
+        p.q.p = (void*)q;
+        p.s.p = (void*)scales;
+        p.bias.p = (void*)bias;
+        try {
+            if (mode == LTX_MODE_F32) {
+                if (!out_f32) throw ltx::Error("mode F32 writes f32 output");
+                LtxAda ada{};
+                ltx::gemm32(c, p, 0, N, (const float*)a, M, (float*)y, LTX_EPI_STORE, nullptr, ada, 0, gelu,
+                            (hipStream_t)stream);
+            } else {
+                LtxGemmArgs g{};
+                g.out = y;
+                g.ldo = N;
+                g.gelu = gelu;
+                g.out_f32 = out_f32;
+                ltx::gemm16(c, mode, p, a, M, K, LTX_EPI_STORE, g, (hipStream_t)stream);
+            }
+        } catch (...) {
+            p.q.p = p.s.p = p.bias.p = nullptr;
+            throw;
+        }
+        p.q.p = p.s.p = p.bias.p = nullptr;
+    })
+}
+
+int ltx_op_attention(ltx_ctx* c, const void* q, const void* k, const void* v, const float* glog, void* out, int lq,
+                     int lkv, int mode, void* stream) {
+    LTX_GUARD(c, {
+        if (!c) throw ltx::Error("NULL context");
+        if (lq <= 0 || lkv <= 0) throw ltx::Error("bad attention lengths");
+        HIPC(hipSetDevice(c->device));
+        if (mode == LTX_MODE_F32)
+            ltx::attn32(c, (const float*)q, (const float*)k, (const float*)v, glog, (float*)out, lq, lkv,
+                        (hipStream_t)stream);
+        else
+            ltx::attn16(c, mode, q, k, v, glog, out, lq, lkv, (hipStream_t)stream);
+    })
+}
+
+int ltx_op_dequant(ltx_ctx* c, const int8_t* q, const void* scales, int scale_f16, int N, int K, float* out32,
+                   void* out16, int mode, void* stream) {
+    LTX_GUARD(c, {
+        if (!c) throw ltx::Error("NULL context");
+        if (N <= 0 || K <= 0 || K % 128) throw ltx::Error("bad dequant shape");
+        HIPC(hipSetDevice(c->device));
+        LtxDequantArgs a{q, scales, out32, out16, N, K, scale_f16};
+        size_t n = (size_t)N * K;
+        c->launch(mode == LTX_MODE_BF16 ? "ltx_dequant_bf16" : "ltx_dequant_f16", (unsigned)((n / 2 + 255) / 256), 1,
+                  1, 256, &a, (hipStream_t)stream);
+    })
+}
+
+}  // extern "C"

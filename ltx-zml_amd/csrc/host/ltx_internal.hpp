@@ -1,0 +1,114 @@
+// Internal declarations of the host runtime (not part of the C ABI).
+#pragma once
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <map>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../ltx_args.h"
+#include "ltx_block.h"
+
+namespace ltx {
+
+// Error carried across internal calls; converted to a status + message at
+// the C boundary and never propagated through it.
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+// Checked HIP call, with the LTX_FAIL_AFTER fault-injection counter.
+void hip_check(hipError_t e, const char* what);
+#define HIPC(x) ::ltx::hip_check((x), #x)
+
+// A device allocation owned by the runtime.
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    void alloc(size_t n);
+    void free_();
+    ~DevBuf() { free_(); }
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+};
+
+struct ProfRec {
+    const char* name;
+    hipEvent_t a, b;
+};
+
+}  // namespace ltx
+
+// One projection's weights on device, in the form the kernels consume.
+struct LtxProj {
+    int N = 0, K = 0;
+    bool q8 = false;          // int8 + scales available
+    int scale_f16 = 0;
+    ltx::DevBuf q;            // int8 [N][K]
+    ltx::DevBuf s;            // [N][K/128] f32 or f16
+    ltx::DevBuf w_bf16;       // bf16 [N][K] (base tensor)
+    ltx::DevBuf w_f16;        // f16 copy of the base tensor (F16 mode, non-q8)
+    ltx::DevBuf bias;         // f32 [N] (may be empty)
+};
+
+struct ltx_block_weights {
+    LtxProj qkv1;             // q1 | k1 | v1, N = 12288
+    LtxProj o1;
+    LtxProj q2;
+    LtxProj kv2;              // k2 | v2, N = 8192
+    LtxProj o2;
+    LtxProj f1, f2;
+    LtxProj g1, g2;           // gate logits, N = 32 (16-bit only)
+    ltx::DevBuf qn1, kn1, qn2, kn2;  // f32 [4096]
+    ltx::DevBuf sst, psst;    // f32 [9][4096], [2][4096]
+    // f32-mode views of the fused projections' parts (bf16 originals / q8)
+    uint64_t bytes = 0;
+};
+
+struct ltx_ctx {
+    int device = 0;
+    std::vector<hipModule_t> modules;
+    std::map<std::string, hipFunction_t> fns;
+    std::string err;
+    // workspace
+    ltx::DevBuf ws;
+    size_t ws_T = 0, ws_S = 0;
+    int ws_mode = -1;
+    void* stage_ptr[LTX_ST_COUNT] = {};
+    uint64_t stage_bytes[LTX_ST_COUNT] = {};
+    // profiling
+    bool prof = false;
+    std::vector<ltx::ProfRec> prof_recs;
+    std::vector<hipEvent_t> ev_pool;
+    hipFunction_t fn(const char* name);
+    // `label` names the launch in the event profile (defaults to the kernel name).
+    void launch(const char* name, unsigned gx, unsigned gy, unsigned gz, unsigned bx, void* args, hipStream_t st,
+                const char* label = nullptr);
+};
+
+namespace ltx {
+void set_thread_error(const std::string& e);
+void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const float* tstab, int K,
+                   const int32_t* tidx, const float* ctxv, int S, const float* pts2, const float* cs,
+                   const float* sn, int T, float* y, int mode, hipStream_t st);
+uint16_t f32_to_f16_bits(float f);
+float bf16_bits_to_f32(uint16_t b);
+}  // namespace ltx
+
+// Runs a body at the C boundary: exceptions become LTX_FAIL + error text.
+#define LTX_GUARD(ctxp, ...)                                    \
+    try {                                                       \
+        __VA_ARGS__;                                            \
+        return LTX_OK;                                          \
+    } catch (const std::exception& ex) {                        \
+        if (ctxp) (ctxp)->err = ex.what();                      \
+        ::ltx::set_thread_error(ex.what());                     \
+        return LTX_FAIL;                                        \
+    } catch (...) {                                             \
+        if (ctxp) (ctxp)->err = "unknown C++ exception";        \
+        ::ltx::set_thread_error("unknown C++ exception");       \
+        return LTX_FAIL;                                        \
+    }

@@ -1,0 +1,274 @@
+// Weight upload: host pointers or a blob image + manifest -> the device form
+// the kernels consume (ltx/loader.zig:100-172: normalizeName, findEntry,
+// buildBlockBufs, buildQuantBufs).
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "json.hpp"
+#include "ltx_internal.hpp"
+
+namespace ltx {
+
+// File stems of WEIGHT_SPECS (ltx/block.zig:377-406), in LTX_W_* order.
+static const char* const kBaseStems[LTX_W_COUNT] = {
+    "attn1_to_q_weight", "attn1_to_q_bias", "attn1_to_k_weight", "attn1_to_k_bias",
+    "attn1_to_v_weight", "attn1_to_v_bias", "attn1_to_out_0_weight", "attn1_to_out_0_bias",
+    "attn1_q_norm_weight", "attn1_k_norm_weight", "attn1_to_gate_logits_weight", "attn1_to_gate_logits_bias",
+    "attn2_to_q_weight", "attn2_to_q_bias", "attn2_to_k_weight", "attn2_to_k_bias",
+    "attn2_to_v_weight", "attn2_to_v_bias", "attn2_to_out_0_weight", "attn2_to_out_0_bias",
+    "attn2_q_norm_weight", "attn2_k_norm_weight", "attn2_to_gate_logits_weight", "attn2_to_gate_logits_bias",
+    "ff_net_0_proj_weight", "ff_net_2_weight", "scale_shift_table", "prompt_scale_shift_table"};
+
+static size_t base_numel(int i) {
+    switch (i) {
+        case LTX_W_G1_W: case LTX_W_G2_W: return (size_t)LTX_H * LTX_D;
+        case LTX_W_G1_B: case LTX_W_G2_B: return LTX_H;
+        case LTX_W_FF1_W: case LTX_W_FF2_W: return (size_t)LTX_FF * LTX_D;
+        case LTX_W_SST: return 9 * (size_t)LTX_D;
+        case LTX_W_PSST: return 2 * (size_t)LTX_D;
+        case LTX_W_Q1_W: case LTX_W_K1_W: case LTX_W_V1_W: case LTX_W_O1_W:
+        case LTX_W_Q2_W: case LTX_W_K2_W: case LTX_W_V2_W: case LTX_W_O2_W: return (size_t)LTX_D * LTX_D;
+        default: return LTX_D;  // biases and norm weights
+    }
+}
+
+// Q8 companions: the base weight each one quantises, and its [O, I].
+static const int kQBase[LTX_Q_COUNT] = {LTX_W_Q1_W, LTX_W_K1_W, LTX_W_V1_W, LTX_W_Q2_W, LTX_W_K2_W,
+                                        LTX_W_V2_W, LTX_W_FF1_W, LTX_W_FF2_W, LTX_W_O1_W, LTX_W_O2_W};
+
+static void q_dims(int qi, int& O, int& I) {
+    O = LTX_D;
+    I = LTX_D;
+    if (qi == LTX_Q_F1) O = LTX_FF;
+    if (qi == LTX_Q_F2) I = LTX_FF;
+}
+
+static void h2d(DevBuf& d, const void* src, size_t n) {
+    d.alloc(n);
+    HIPC(hipMemcpy(d.p, src, n, hipMemcpyHostToDevice));
+}
+
+static std::vector<float> bf16v_to_f32(const uint16_t* p, size_t n) {
+    std::vector<float> o(n);
+    for (size_t i = 0; i < n; i++) o[i] = bf16_bits_to_f32(p[i]);
+    return o;
+}
+
+static std::vector<uint16_t> bf16v_to_f16(const uint16_t* p, size_t n) {
+    std::vector<uint16_t> o(n);
+    for (size_t i = 0; i < n; i++) o[i] = f32_to_f16_bits(bf16_bits_to_f32(p[i]));
+    return o;
+}
+
+// One projection from parts (fused along N when several are given).
+static void build_proj(LtxProj& p, const void* const* base, const int8_t* const* q8, const void* const* q8s, int sf16,
+                       std::initializer_list<int> qids, int K, bool want_f16_copy) {
+    std::vector<int> ids(qids);
+    bool all_q8 = q8 != nullptr && q8s != nullptr;
+    if (all_q8)
+        for (int qi : ids) all_q8 = all_q8 && q8[qi] && q8s[qi];
+    p.K = K;
+    p.N = 0;
+    std::vector<int> Ns;
+    for (int qi : ids) {
+        int O, I;
+        q_dims(qi, O, I);
+        Ns.push_back(O);
+        p.N += O;
+    }
+    p.q8 = all_q8;
+    p.scale_f16 = sf16;
+    const size_t G = K / LTX_GROUP;
+    if (all_q8) {
+        std::vector<int8_t> q((size_t)p.N * K);
+        std::vector<char> s((size_t)p.N * G * (sf16 ? 2 : 4));
+        size_t r = 0;
+        for (size_t j = 0; j < ids.size(); j++) {
+            int qi = ids[j];
+            std::memcpy(q.data() + r * K, q8[qi], (size_t)Ns[j] * K);
+            std::memcpy(s.data() + r * G * (sf16 ? 2 : 4), q8s[qi], (size_t)Ns[j] * G * (sf16 ? 2 : 4));
+            r += Ns[j];
+        }
+        h2d(p.q, q.data(), q.size());
+        h2d(p.s, s.data(), s.size());
+    } else {
+        std::vector<uint16_t> w((size_t)p.N * K);
+        size_t r = 0;
+        for (size_t j = 0; j < ids.size(); j++) {
+            std::memcpy(w.data() + r * K, base[kQBase[ids[j]]], (size_t)Ns[j] * K * 2);
+            r += Ns[j];
+        }
+        h2d(p.w_bf16, w.data(), w.size() * 2);
+        if (want_f16_copy) {
+            auto h = bf16v_to_f16(w.data(), w.size());
+            h2d(p.w_f16, h.data(), h.size() * 2);
+        }
+    }
+    // biases: weight slot + 1 in WEIGHT_SPECS order for the attention projections
+    std::vector<float> b;
+    bool has_bias = false;
+    for (int qi : ids) {
+        int bw = kQBase[qi];
+        bool biased = bw != LTX_W_FF1_W && bw != LTX_W_FF2_W;  // the video FFN is bias-free
+        int O, I;
+        q_dims(qi, O, I);
+        if (biased) {
+            has_bias = true;
+            auto v = bf16v_to_f32((const uint16_t*)base[bw + 1], O);
+            b.insert(b.end(), v.begin(), v.end());
+        } else {
+            b.insert(b.end(), O, 0.0f);
+        }
+    }
+    if (has_bias) h2d(p.bias, b.data(), b.size() * 4);
+}
+
+static void build_gate(LtxProj& p, const void* const* base, int wi) {
+    p.N = LTX_H;
+    p.K = LTX_D;
+    const uint16_t* w = (const uint16_t*)base[wi];
+    h2d(p.w_bf16, w, (size_t)LTX_H * LTX_D * 2);
+    auto h = bf16v_to_f16(w, (size_t)LTX_H * LTX_D);
+    h2d(p.w_f16, h.data(), h.size() * 2);
+    auto b = bf16v_to_f32((const uint16_t*)base[wi + 1], LTX_H);
+    h2d(p.bias, b.data(), b.size() * 4);
+}
+
+static uint64_t proj_bytes(const LtxProj& p) {
+    return p.q.bytes + p.s.bytes + p.w_bf16.bytes + p.w_f16.bytes + p.bias.bytes;
+}
+
+ltx_block_weights* upload(ltx_ctx* c, const void* const* base, const int8_t* const* q8, const void* const* q8s, int sf16) {
+    if (!base) throw Error("NULL base weight table");
+    for (int i = 0; i < LTX_W_COUNT; i++)
+        if (!base[i]) throw Error(std::string("missing base weight ") + kBaseStems[i]);
+    HIPC(hipSetDevice(c->device));
+    auto* w = new ltx_block_weights();
+    try {
+        build_proj(w->qkv1, base, q8, q8s, sf16, {LTX_Q_Q1, LTX_Q_K1, LTX_Q_V1}, LTX_D, true);
+        build_proj(w->o1, base, q8, q8s, sf16, {LTX_Q_O1}, LTX_D, true);
+        build_proj(w->q2, base, q8, q8s, sf16, {LTX_Q_Q2}, LTX_D, true);
+        build_proj(w->kv2, base, q8, q8s, sf16, {LTX_Q_K2, LTX_Q_V2}, LTX_D, true);
+        build_proj(w->o2, base, q8, q8s, sf16, {LTX_Q_O2}, LTX_D, true);
+        build_proj(w->f1, base, q8, q8s, sf16, {LTX_Q_F1}, LTX_D, true);
+        build_proj(w->f2, base, q8, q8s, sf16, {LTX_Q_F2}, LTX_FF, true);
+        build_gate(w->g1, base, LTX_W_G1_W);
+        build_gate(w->g2, base, LTX_W_G2_W);
+        auto up_f32 = [&](DevBuf& d, int wi) {
+            auto v = bf16v_to_f32((const uint16_t*)base[wi], LTX_D);
+            h2d(d, v.data(), v.size() * 4);
+        };
+        up_f32(w->qn1, LTX_W_QN1);
+        up_f32(w->kn1, LTX_W_KN1);
+        up_f32(w->qn2, LTX_W_QN2);
+        up_f32(w->kn2, LTX_W_KN2);
+        h2d(w->sst, base[LTX_W_SST], 9 * (size_t)LTX_D * 4);
+        h2d(w->psst, base[LTX_W_PSST], 2 * (size_t)LTX_D * 4);
+        w->bytes = proj_bytes(w->qkv1) + proj_bytes(w->o1) + proj_bytes(w->q2) + proj_bytes(w->kv2) +
+                   proj_bytes(w->o2) + proj_bytes(w->f1) + proj_bytes(w->f2) + proj_bytes(w->g1) + proj_bytes(w->g2) +
+                   w->qn1.bytes * 4 + w->sst.bytes + w->psst.bytes;
+    } catch (...) {
+        delete w;
+        throw;
+    }
+    return w;
+}
+
+// '.' -> '_', "::" -> '_' (ltx/loader.zig:100-119)
+std::string normalize_name(const std::string& n) {
+    std::string o;
+    for (size_t i = 0; i < n.size(); i++) {
+        if (n[i] == ':' && i + 1 < n.size() && n[i + 1] == ':') {
+            o.push_back('_');
+            i++;
+        } else if (n[i] == '.') {
+            o.push_back('_');
+        } else {
+            o.push_back(n[i]);
+        }
+    }
+    return o;
+}
+
+struct Entry {
+    std::string dtype;
+    uint64_t offset, nbytes;
+};
+
+ltx_block_weights* upload_blob(ltx_ctx* c, const void* mem, uint64_t mem_bytes, const char* manifest, int64_t block) {
+    if (!mem || !manifest) throw Error("NULL blob or manifest");
+    json::Value m = json::parse(manifest);
+    std::unordered_map<std::string, Entry> ents;
+    for (const auto& e : m.at("entries").arr) {
+        Entry en{e.at("dtype").as_str(), (uint64_t)e.at("offset").as_int(), (uint64_t)e.at("nbytes").as_int()};
+        if (en.offset + en.nbytes > mem_bytes) throw Error("manifest entry beyond the blob: " + e.at("name").as_str());
+        ents[normalize_name(e.at("name").as_str())] = en;
+    }
+    const char* bytes = (const char*)mem;
+    auto find = [&](const std::string& want) -> const Entry* {
+        auto it = ents.find(want);
+        return it == ents.end() ? nullptr : &it->second;
+    };
+    const std::string pre = "transformer_blocks_" + std::to_string(block) + "_";
+    const void* base[LTX_W_COUNT];
+    for (int i = 0; i < LTX_W_COUNT; i++) {
+        const Entry* e = find(pre + kBaseStems[i]);
+        if (!e) throw Error("blob " + std::to_string(block) + ": no entry named " + pre + kBaseStems[i]);
+        bool f32 = i == LTX_W_SST || i == LTX_W_PSST;
+        if (e->dtype != (f32 ? "F32" : "BF16")) throw Error("unexpected dtype " + e->dtype + " for " + kBaseStems[i]);
+        if (e->nbytes != base_numel(i) * (f32 ? 4 : 2)) throw Error(std::string("size mismatch for ") + kBaseStems[i]);
+        base[i] = bytes + e->offset;
+    }
+    const int8_t* q8[LTX_Q_COUNT] = {};
+    const void* q8s[LTX_Q_COUNT] = {};
+    int sf16 = -1;
+    for (int qi = 0; qi < LTX_Q_COUNT; qi++) {
+        std::string stem = pre + kBaseStems[kQBase[qi]];
+        const Entry* eq = find(stem + "_q8");
+        const Entry* es = find(stem + "_q8scale");
+        if (!eq || !es) continue;
+        int O, I;
+        q_dims(qi, O, I);
+        if (eq->dtype != "I8" || eq->nbytes != (uint64_t)O * I) throw Error("bad q8 entry " + stem);
+        int f16 = es->dtype == "F16" ? 1 : es->dtype == "F32" ? 0 : -1;
+        if (f16 < 0) throw Error("bad q8scale dtype " + es->dtype);
+        if (sf16 >= 0 && f16 != sf16) throw Error("mixed q8scale dtypes in one blob");
+        sf16 = f16;
+        if (es->nbytes != (uint64_t)O * (I / LTX_GROUP) * (f16 ? 2 : 4)) throw Error("bad q8scale size " + stem);
+        q8[qi] = (const int8_t*)(bytes + eq->offset);
+        q8s[qi] = bytes + es->offset;
+    }
+    return upload(c, base, q8, q8s, sf16 < 0 ? 0 : sf16);
+}
+
+}  // namespace ltx
+
+
+extern "C" {
+
+int ltx_block_weights_from_host(ltx_ctx* c, const void* const* base, const int8_t* const* q8, const void* const* q8s,
+                                int scale_f16, ltx_block_weights** out) {
+    LTX_GUARD(c, {
+        if (!c || !out) throw ltx::Error("NULL context or out");
+        *out = ltx::upload(c, base, q8, q8s, scale_f16);
+    })
+}
+
+int ltx_block_weights_from_blob(ltx_ctx* c, const void* mem, uint64_t mem_bytes, const char* manifest_json,
+                                int64_t block_idx, ltx_block_weights** out) {
+    LTX_GUARD(c, {
+        if (!c || !out) throw ltx::Error("NULL context or out");
+        *out = ltx::upload_blob(c, mem, mem_bytes, manifest_json, block_idx);
+    })
+}
+
+void ltx_block_weights_free(ltx_ctx* c, ltx_block_weights* w) {
+    if (c) (void)hipSetDevice(c->device);
+    delete w;
+}
+
+uint64_t ltx_block_weights_bytes(const ltx_block_weights* w) { return w ? w->bytes : 0; }
+
+}  // extern "C"

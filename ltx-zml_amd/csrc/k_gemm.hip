@@ -1,0 +1,239 @@
+// W8A16 / W16A16 GEMM for gfx950: y[M][N] = A[M][K] . W[N][K]^T with fused
+// epilogues (bias, GELU-tanh, gated residual, QKV split with V^T store).
+//
+// Tile 256 x 256 x 64, 256 threads = 4 waves in a 2 x 2 grid, each wave owning
+// a 128 x 128 sub-tile = 4 x 4 MFMA blocks of v_mfma_f32_32x32x16_{f16,bf16}
+// (fp32 accumulate). Global -> register -> LDS staging with two LDS buffers
+// and one barrier per K-tile. int8 weights are dequantised ONCE per workgroup
+// while staging into LDS: v = fma(u, s, -128 s) with u = q + 128 (an unsigned
+// byte), which is the single-rounding f32 value q * s of dq4
+// (ltx/block.zig:462-471), then rounded to the 16-bit operand type.
+// LDS rows are padded by 16 bytes so the 32 rows a fragment read touches hit
+// distinct banks.
+#include "ltx_device.h"
+
+#define BM 256
+#define BN 256
+#define BK 64
+#define LDSW (BK + 8)  // 16-bit elements per padded LDS row
+#define GM 8           // M-tiles per rasterisation group
+
+struct TileIdx {
+    int tm, tn;
+};
+
+// Hardware places workgroup b on XCD b % 8. Hand each XCD a contiguous run of
+// the tile sequence, and walk that sequence in groups of GM M-tiles x all
+// N-tiles, so the ~32 workgroups resident on one XCD share A rows and B
+// columns in that XCD's L2.
+__device__ __forceinline__ TileIdx tile_of(int bid, int tiles_m, int tiles_n) {
+    int nt = tiles_m * tiles_n;
+    int t = bid;
+    if ((nt & 7) == 0) t = (bid & 7) * (nt >> 3) + (bid >> 3);
+    int gsz = GM * tiles_n;
+    int g = t / gsz, r = t - g * gsz;
+    int gm0 = g * GM;
+    int gcnt = min(GM, tiles_m - gm0);
+    TileIdx ti;
+    ti.tm = gm0 + r % gcnt;
+    ti.tn = r / gcnt;
+    return ti;
+}
+
+template <typename T, int BKIND>
+struct Stage {
+    // A: 8 x 16 B per thread; B: int8 4 x 16 B, or 16-bit 8 x 16 B.
+    u32x4 ra[8];
+    u32x4 rb[8];
+    float sc[4];
+
+    __device__ __forceinline__ void load(const LtxGemmArgs& a, int m0, int n0, int k0, int tid) {
+        const uint16_t* A = (const uint16_t*)a.a;
+        int c = tid & 7;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            int r = min(m0 + (tid >> 3) + 32 * i, a.M - 1);
+            ra[i] = *(const u32x4*)(A + (size_t)r * a.lda + k0 + 8 * c);
+        }
+        if (BKIND == LTX_B_W16) {
+            const uint16_t* B = (const uint16_t*)a.b;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                int r = n0 + (tid >> 3) + 32 * i;
+                rb[i] = *(const u32x4*)(B + (size_t)r * a.K + k0 + 8 * c);
+            }
+        } else {
+            const int8_t* B = (const int8_t*)a.b;
+            int cb = tid & 3;
+            int G = a.K / LTX_GROUP;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                int r = n0 + (tid >> 2) + 64 * i;
+                rb[i] = *(const u32x4*)(B + (size_t)r * a.K + k0 + 16 * cb);
+                size_t si = (size_t)r * G + (k0 + 16 * cb) / LTX_GROUP;
+                sc[i] = BKIND == LTX_B_I8_F16S ? f16_bits_to_f32(((const uint16_t*)a.scales)[si])
+                                              : ((const float*)a.scales)[si];
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(uint16_t* sA, uint16_t* sB, int tid) {
+        int c = tid & 7;
+#pragma unroll
+        for (int i = 0; i < 8; i++) *(u32x4*)(sA + ((tid >> 3) + 32 * i) * LDSW + 8 * c) = ra[i];
+        if (BKIND == LTX_B_W16) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) *(u32x4*)(sB + ((tid >> 3) + 32 * i) * LDSW + 8 * c) = rb[i];
+        } else {
+            int cb = tid & 3;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float s = sc[i], nb = -128.0f * s;
+                uint32_t o[8];
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    uint32_t w = rb[i][d] ^ 0x80808080u;
+                    o[2 * d] = deq_pack2<T>((float)(w & 0xffu), (float)((w >> 8) & 0xffu), s, nb);
+                    o[2 * d + 1] = deq_pack2<T>((float)((w >> 16) & 0xffu), (float)(w >> 24), s, nb);
+                }
+                uint16_t* dst = sB + ((tid >> 2) + 64 * i) * LDSW + 16 * cb;
+                *(u32x4*)dst = u32x4{o[0], o[1], o[2], o[3]};
+                *(u32x4*)(dst + 8) = u32x4{o[4], o[5], o[6], o[7]};
+            }
+        }
+    }
+};
+
+template <typename T, int BKIND, int EPI>
+__device__ void gemm_body(const LtxGemmArgs& a) {
+    typedef typename Op<T>::v8 v8;
+    __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * LDSW];
+    __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN * LDSW];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int wm = w >> 1, wn = w & 1;
+    TileIdx ti = tile_of(blockIdx.x, a.tiles_m, a.tiles_n);
+    const int m0 = ti.tm * BM, n0 = ti.tn * BN;
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x16{0};
+
+    Stage<T, BKIND> st;
+    const int nk = a.K / BK;
+    st.load(a, m0, n0, 0, tid);
+    st.store(sA[0], sB[0], tid);
+    __syncthreads();
+
+    const int fr = lane & 31, fk = 8 * (lane >> 5);
+    for (int kt = 0; kt < nk; kt++) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) st.load(a, m0, n0, (kt + 1) * BK, tid);
+        const uint16_t* pa = sA[buf] + (wm * 128 + fr) * LDSW + fk;
+        const uint16_t* pb = sB[buf] + (wn * 128 + fr) * LDSW + fk;
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; kk++) {
+            v8 fa[4], fb[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) fa[i] = __builtin_bit_cast(v8, *(const u32x4*)(pa + 32 * i * LDSW + 16 * kk));
+#pragma unroll
+            for (int j = 0; j < 4; j++) fb[j] = __builtin_bit_cast(v8, *(const u32x4*)(pb + 32 * j * LDSW + 16 * kk));
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = Op<T>::mfma32(fa[i], fb[j], acc[i][j]);
+        }
+        if (kt + 1 < nk) st.store(sA[buf ^ 1], sB[buf ^ 1], tid);
+        __syncthreads();
+    }
+
+    // Epilogue. acc[i][j][r] sits at row 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4
+    // and column 32 j + lane % 32 of this wave's 128 x 128 sub-tile.
+    const int rb = m0 + wm * 128 + 4 * (lane >> 5);
+    const int cb = n0 + wn * 128 + (lane & 31);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = cb + 32 * j;
+        const float bias = a.bias ? a.bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = rb + 32 * i + 8 * (r >> 2) + (r & 3);
+                if (m >= a.M) continue;
+                float v = acc[i][j][r] + bias;
+                if (EPI == LTX_EPI_STORE) {
+                    if (a.gelu) v = gelu_tanh(v);
+                    if (a.out_f32)
+                        ((float*)a.out)[(size_t)m * a.ldo + n] = v;
+                    else
+                        ((uint16_t*)a.out)[(size_t)m * a.ldo + n] = Op<T>::bits(v);
+                } else if (EPI == LTX_EPI_RESID_GATE) {
+                    size_t o = (size_t)m * a.ldo + n;
+                    ((float*)a.out)[o] = a.resid[o] + v * ada_val(a.ada, m, a.igate, n);
+                } else {  // QKV
+                    if (n0 < a.nsplit) {
+                        ((float*)a.out)[(size_t)m * a.nsplit + n] = v;
+                    } else {
+                        int c = n - a.nsplit;  // = h * 128 + d
+                        ((uint16_t*)a.out2)[(size_t)c * a.M + m] = Op<T>::bits(v);
+                    }
+                }
+            }
+        }
+    }
+}
+
+#define GEMM_KERNEL(NAME, T, BK_, EPI_)                                                        \
+    extern "C" __global__ void __launch_bounds__(256, 1) NAME(const LtxGemmArgs a) {           \
+        gemm_body<T, BK_, EPI_>(a);                                                            \
+    }
+
+GEMM_KERNEL(ltx_gemm_f16_i8f32_store, _Float16, LTX_B_I8_F32S, LTX_EPI_STORE)
+GEMM_KERNEL(ltx_gemm_f16_i8f32_resid, _Float16, LTX_B_I8_F32S, LTX_EPI_RESID_GATE)
+GEMM_KERNEL(ltx_gemm_f16_i8f32_qkv, _Float16, LTX_B_I8_F32S, LTX_EPI_QKV)
+GEMM_KERNEL(ltx_gemm_f16_i8f16_store, _Float16, LTX_B_I8_F16S, LTX_EPI_STORE)
+GEMM_KERNEL(ltx_gemm_f16_i8f16_resid, _Float16, LTX_B_I8_F16S, LTX_EPI_RESID_GATE)
+GEMM_KERNEL(ltx_gemm_f16_i8f16_qkv, _Float16, LTX_B_I8_F16S, LTX_EPI_QKV)
+GEMM_KERNEL(ltx_gemm_f16_w16_store, _Float16, LTX_B_W16, LTX_EPI_STORE)
+GEMM_KERNEL(ltx_gemm_f16_w16_resid, _Float16, LTX_B_W16, LTX_EPI_RESID_GATE)
+GEMM_KERNEL(ltx_gemm_bf16_i8f32_store, __bf16, LTX_B_I8_F32S, LTX_EPI_STORE)
+GEMM_KERNEL(ltx_gemm_bf16_i8f32_resid, __bf16, LTX_B_I8_F32S, LTX_EPI_RESID_GATE)
+GEMM_KERNEL(ltx_gemm_bf16_i8f32_qkv, __bf16, LTX_B_I8_F32S, LTX_EPI_QKV)
+GEMM_KERNEL(ltx_gemm_bf16_i8f16_store, __bf16, LTX_B_I8_F16S, LTX_EPI_STORE)
+GEMM_KERNEL(ltx_gemm_bf16_i8f16_resid, __bf16, LTX_B_I8_F16S, LTX_EPI_RESID_GATE)
+GEMM_KERNEL(ltx_gemm_bf16_i8f16_qkv, __bf16, LTX_B_I8_F16S, LTX_EPI_QKV)
+GEMM_KERNEL(ltx_gemm_bf16_w16_store, __bf16, LTX_B_W16, LTX_EPI_STORE)
+GEMM_KERNEL(ltx_gemm_bf16_w16_resid, __bf16, LTX_B_W16, LTX_EPI_RESID_GATE)
+
+// Gate logits (ltx/block.zig:238, 526, 564): glog[t][h] = a[t] . gw[h] + gb[h].
+// One wave per 32 token rows: 256 MFMAs over K = 4096, operands straight
+// from global memory (the 32 x 4096 weight stays L2-resident).
+template <typename T>
+__device__ void gate_body(const LtxGateArgs& a) {
+    typedef typename Op<T>::v8 v8;
+    const int lane = threadIdx.x & 63;
+    const int m0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 32;
+    if (m0 >= a.M) return;
+    const int fr = lane & 31, fk = 8 * (lane >> 5);
+    const uint16_t* pa = (const uint16_t*)a.a + (size_t)min(m0 + fr, a.M - 1) * LTX_D + fk;
+    const uint16_t* pb = (const uint16_t*)a.gw + (size_t)fr * LTX_D + fk;
+    f32x16 acc = f32x16{0};
+#pragma unroll 8
+    for (int k = 0; k < LTX_D; k += 16) {
+        v8 fa = __builtin_bit_cast(v8, *(const u32x4*)(pa + k));
+        v8 fb = __builtin_bit_cast(v8, *(const u32x4*)(pb + k));
+        acc = Op<T>::mfma32(fa, fb, acc);
+    }
+    const float bias = a.gb[fr];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        int m = m0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < a.M) a.out[(size_t)m * LTX_H + fr] = acc[r] + bias;
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) ltx_gate_f16(const LtxGateArgs a) { gate_body<_Float16>(a); }
+extern "C" __global__ void __launch_bounds__(256) ltx_gate_bf16(const LtxGateArgs a) { gate_body<__bf16>(a); }

@@ -1,0 +1,197 @@
+// Bandwidth-bound kernels: fused RMSNorm + AdaLN modulate, the cross-attention
+// K/V modulation, and the full-row qk RMSNorm + split-half 3D RoPE.
+// One 256-thread workgroup per token row of D = 4096 channels.
+#include "ltx_device.h"
+
+// RMSNorm + modulate (ltx/block.zig:28-30, 36-38, 248-252, 548-552, 569-572):
+// y = x * rsqrt(mean(x^2) + 1e-6) * (1 + ada[isc]) + ada[ish].
+// Each thread owns 4 float4 columns c = 4*tid + 1024*i.
+template <int OUT>  // 0: f16, 1: bf16, 2: f32
+__device__ void norm_mod_body(const LtxNormArgs& a) {
+    __shared__ float red[4];
+    int row = blockIdx.x;
+    if (row >= a.rows) return;
+    const float4* x = (const float4*)(a.x + (size_t)row * LTX_D);
+    float4 v[4];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[i] = x[threadIdx.x + 256 * i];
+        ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    }
+    ss = block_sum256(ss, red);
+    float inv = 1.0f / sqrtf(ss * (1.0f / LTX_D) + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int c = 4 * (threadIdx.x + 256 * i);
+        float o[4] = {v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv};
+        if (a.isc >= 0) {
+            int r = a.ada.tidx[row];
+            const float4 sc_t = *(const float4*)(a.ada.tstab + ((size_t)r * 9 + a.isc) * LTX_D + c);
+            const float4 sc_s = *(const float4*)(a.ada.sst + (size_t)a.isc * LTX_D + c);
+            const float4 sh_t = *(const float4*)(a.ada.tstab + ((size_t)r * 9 + a.ish) * LTX_D + c);
+            const float4 sh_s = *(const float4*)(a.ada.sst + (size_t)a.ish * LTX_D + c);
+            float sc[4] = {sc_t.x + sc_s.x, sc_t.y + sc_s.y, sc_t.z + sc_s.z, sc_t.w + sc_s.w};
+            float sh[4] = {sh_t.x + sh_s.x, sh_t.y + sh_s.y, sh_t.z + sh_s.z, sh_t.w + sh_s.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) o[j] = o[j] * (sc[j] + 1.0f) + sh[j];
+        }
+        size_t off = (size_t)row * LTX_D + c;
+        if (OUT == 2) {
+            *(float4*)((float*)a.y + off) = make_float4(o[0], o[1], o[2], o[3]);
+        } else if (OUT == 0) {
+            u32x2 p = {pack2<_Float16>(o[0], o[1]), pack2<_Float16>(o[2], o[3])};
+            *(u32x2*)((uint16_t*)a.y + off) = p;
+        } else {
+            u32x2 p = {pack2<__bf16>(o[0], o[1]), pack2<__bf16>(o[2], o[3])};
+            *(u32x2*)((uint16_t*)a.y + off) = p;
+        }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) ltx_norm_mod_f16(const LtxNormArgs a) { norm_mod_body<0>(a); }
+extern "C" __global__ void __launch_bounds__(256) ltx_norm_mod_bf16(const LtxNormArgs a) { norm_mod_body<1>(a); }
+extern "C" __global__ void __launch_bounds__(256) ltx_norm_mod_f32(const LtxNormArgs a) { norm_mod_body<2>(a); }
+
+// enc = ctx * (1 + (psst[1] + pts2[1])) + (psst[0] + pts2[0])  (ltx/block.zig:553-556)
+template <int OUT>
+__device__ void enc_body(const LtxEncArgs& a) {
+    int row = blockIdx.x;
+    if (row >= a.rows) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int c = 4 * (threadIdx.x + 256 * i);
+        float4 x = *(const float4*)(a.ctx + (size_t)row * LTX_D + c);
+        float4 s0 = *(const float4*)(a.psst + c), s1 = *(const float4*)(a.psst + LTX_D + c);
+        float4 p0 = *(const float4*)(a.pts2 + c), p1 = *(const float4*)(a.pts2 + LTX_D + c);
+        float o[4] = {x.x * ((s1.x + p1.x) + 1.0f) + (s0.x + p0.x), x.y * ((s1.y + p1.y) + 1.0f) + (s0.y + p0.y),
+                      x.z * ((s1.z + p1.z) + 1.0f) + (s0.z + p0.z), x.w * ((s1.w + p1.w) + 1.0f) + (s0.w + p0.w)};
+        size_t off = (size_t)row * LTX_D + c;
+        if (OUT == 2) {
+            *(float4*)((float*)a.y + off) = make_float4(o[0], o[1], o[2], o[3]);
+        } else if (OUT == 0) {
+            u32x2 p = {pack2<_Float16>(o[0], o[1]), pack2<_Float16>(o[2], o[3])};
+            *(u32x2*)((uint16_t*)a.y + off) = p;
+        } else {
+            u32x2 p = {pack2<__bf16>(o[0], o[1]), pack2<__bf16>(o[2], o[3])};
+            *(u32x2*)((uint16_t*)a.y + off) = p;
+        }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) ltx_enc_f16(const LtxEncArgs a) { enc_body<0>(a); }
+extern "C" __global__ void __launch_bounds__(256) ltx_enc_bf16(const LtxEncArgs a) { enc_body<1>(a); }
+extern "C" __global__ void __launch_bounds__(256) ltx_enc_f32(const LtxEncArgs a) { enc_body<2>(a); }
+
+// qk norm + RoPE (ltx/block.zig:32-34, 69-77, 214-226): y = rope(rms(x) * w).
+// Thread t owns head h = t / 8 and rotary slots f0 = 8 * (t % 8) .. f0 + 8, so
+// each RoPE pair (f, f + 64) lives in one thread. Output head-major [H][rows][HD].
+template <typename T>
+__device__ void qknorm_body(const LtxQkNormArgs& a) {
+    __shared__ float red[4];
+    int row = blockIdx.x;
+    if (row >= a.rows) return;
+    int h = threadIdx.x >> 3, f0 = (threadIdx.x & 7) * 8;
+    const float* xr = a.x + (size_t)row * a.ldx + h * LTX_HD;
+    float lo[8], hi[8];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j += 4) {
+        float4 p = *(const float4*)(xr + f0 + j);
+        float4 q = *(const float4*)(xr + 64 + f0 + j);
+        lo[j] = p.x; lo[j + 1] = p.y; lo[j + 2] = p.z; lo[j + 3] = p.w;
+        hi[j] = q.x; hi[j + 1] = q.y; hi[j + 2] = q.z; hi[j + 3] = q.w;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) ss += lo[j] * lo[j] + hi[j] * hi[j];
+    ss = block_sum256(ss, red);
+    float inv = 1.0f / sqrtf(ss * (1.0f / LTX_D) + 1e-6f);
+    const float* wl = a.w + h * LTX_HD + f0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        lo[j] = lo[j] * inv * wl[j];
+        hi[j] = hi[j] * inv * wl[64 + j];
+    }
+    if (a.cos) {
+        const float* cr = a.cos + ((size_t)row * LTX_H + h) * 64 + f0;
+        const float* sr = a.sin + ((size_t)row * LTX_H + h) * 64 + f0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            float c = cr[j], s = sr[j], x0 = lo[j], x1 = hi[j];
+            lo[j] = x0 * c - x1 * s;
+            hi[j] = x1 * c + x0 * s;
+        }
+    }
+    uint16_t* y = (uint16_t*)a.y + ((size_t)h * a.rows + row) * LTX_HD;
+    u32x4 plo = {pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3]), pack2<T>(lo[4], lo[5]), pack2<T>(lo[6], lo[7])};
+    u32x4 phi = {pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3]), pack2<T>(hi[4], hi[5]), pack2<T>(hi[6], hi[7])};
+    *(u32x4*)(y + f0) = plo;
+    *(u32x4*)(y + 64 + f0) = phi;
+}
+
+extern "C" __global__ void __launch_bounds__(256) ltx_qknorm_f16(const LtxQkNormArgs a) { qknorm_body<_Float16>(a); }
+extern "C" __global__ void __launch_bounds__(256) ltx_qknorm_bf16(const LtxQkNormArgs a) { qknorm_body<__bf16>(a); }
+
+// f32 mode: in place on [rows][ldx] f32, merged-head layout kept.
+extern "C" __global__ void __launch_bounds__(256) ltx_qknorm_f32(const LtxQkNorm32Args a) {
+    __shared__ float red[4];
+    int row = blockIdx.x;
+    if (row >= a.rows) return;
+    int h = threadIdx.x >> 3, f0 = (threadIdx.x & 7) * 8;
+    float* xr = a.x + (size_t)row * a.ldx + h * LTX_HD;
+    float lo[8], hi[8];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        lo[j] = xr[f0 + j];
+        hi[j] = xr[64 + f0 + j];
+        ss += lo[j] * lo[j] + hi[j] * hi[j];
+    }
+    ss = block_sum256(ss, red);
+    float inv = 1.0f / sqrtf(ss * (1.0f / LTX_D) + 1e-6f);
+    const float* wl = a.w + h * LTX_HD + f0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        lo[j] = lo[j] * inv * wl[j];
+        hi[j] = hi[j] * inv * wl[64 + j];
+    }
+    if (a.cos) {
+        const float* cr = a.cos + ((size_t)row * LTX_H + h) * 64 + f0;
+        const float* sr = a.sin + ((size_t)row * LTX_H + h) * 64 + f0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            float c = cr[j], s = sr[j], x0 = lo[j], x1 = hi[j];
+            lo[j] = x0 * c - x1 * s;
+            hi[j] = x1 * c + x0 * s;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        xr[f0 + j] = lo[j];
+        xr[64 + f0 + j] = hi[j];
+    }
+}
+
+// Dequantisation probe: the exact f32 value q * s (one rounding, as dq4 at
+// ltx/block.zig:462-471) and the 16-bit operand the GEMM feeds the MFMA.
+// Same arithmetic as the GEMM's staging path: fma(u, s, -128 s) with
+// u = q + 128 read as an unsigned byte, which equals round(q * s).
+// Each thread handles a pair of adjacent elements (K is a multiple of 128).
+template <typename T>
+__device__ void dequant_body(const LtxDequantArgs& a) {
+    size_t i = 2 * ((size_t)blockIdx.x * blockDim.x + threadIdx.x);
+    size_t n = (size_t)a.N * a.K;
+    if (i >= n) return;
+    int row = (int)(i / a.K), k = (int)(i % a.K);
+    size_t si = (size_t)row * (a.K / LTX_GROUP) + k / LTX_GROUP;
+    float s = a.scale_f16 ? f16_bits_to_f32(((const uint16_t*)a.scales)[si]) : ((const float*)a.scales)[si];
+    float nb = -128.0f * s;
+    float u0 = (float)(uint8_t)((uint8_t)a.q[i] ^ 0x80u);
+    float u1 = (float)(uint8_t)((uint8_t)a.q[i + 1] ^ 0x80u);
+    a.out32[i] = __builtin_fmaf(u0, s, nb);
+    a.out32[i + 1] = __builtin_fmaf(u1, s, nb);
+    *(uint32_t*)((uint16_t*)a.out16 + i) = deq_pack2<T>(u0, u1, s, nb);
+}
+
+extern "C" __global__ void __launch_bounds__(256) ltx_dequant_f16(const LtxDequantArgs a) { dequant_body<_Float16>(a); }
+extern "C" __global__ void __launch_bounds__(256) ltx_dequant_bf16(const LtxDequantArgs a) { dequant_body<__bf16>(a); }

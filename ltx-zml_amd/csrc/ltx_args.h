@@ -1,0 +1,161 @@
+// Kernel argument blocks shared by the host orchestrator (g++) and the gfx950
+// code objects (hipcc --genco). Every kernel takes exactly one of these by
+// value, so hipModuleLaunchKernel passes a single pointer in kernelParams.
+// Plain C layout only: pointers, 32/64-bit integers, floats.
+#pragma once
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// Model geometry of the LTX-2.5 video block (ltx/block.zig:14-18).
+#define LTX_D 4096
+#define LTX_H 32
+#define LTX_HD 128
+#define LTX_FF 16384
+#define LTX_GROUP 128
+
+// AdaLN gather (ltx/block.zig:47-67): ada_i[t][c] = sst[i][c] + tstab[tidx[t]][i][c].
+typedef struct {
+    const float* sst;    // [9][D] per-block table
+    const float* tstab;  // [K][9][D] timestep table
+    const int32_t* tidx; // [T] row of tstab per token
+} LtxAda;
+
+// Fused RMSNorm + AdaLN modulate: y = rms(x) * (1 + ada[isc]) + ada[ish].
+typedef struct {
+    const float* x;  // [rows][D] f32
+    void* y;         // [rows][D] f16 / bf16 / f32 (by kernel)
+    LtxAda ada;
+    int rows;
+    int ish, isc;    // ada row indices for shift and scale; isc < 0: plain rms
+} LtxNormArgs;
+
+// Cross-attention K/V modulation (ltx/block.zig:553-556):
+// enc = ctx * (1 + (psst[1] + pts2[1])) + (psst[0] + pts2[0]).
+typedef struct {
+    const float* ctx;   // [S][D]
+    const float* psst;  // [2][D]
+    const float* pts2;  // [2][D]
+    void* y;            // [S][D]
+    int rows;
+} LtxEncArgs;
+
+// Epilogue kinds of the W8A16 / W16A16 GEMM.
+enum {
+    LTX_EPI_STORE = 0,      // y = acc (+ bias); out f32 or 16-bit; optional GELU
+    LTX_EPI_RESID_GATE = 1, // out32 = resid + (acc (+ bias)) * ada[igate]
+    LTX_EPI_QKV = 2,        // cols < nsplit: f32 [M][nsplit] (+bias); cols >= nsplit: 16-bit V^T [H][HD][M]
+};
+
+// B operand kinds.
+enum {
+    LTX_B_I8_F32S = 0,  // int8 [N][K] + f32 scales [N][K/128]
+    LTX_B_I8_F16S = 1,  // int8 [N][K] + f16 scales [N][K/128]
+    LTX_B_W16 = 2,      // 16-bit weights [N][K] in the operand type
+};
+
+typedef struct {
+    const void* a;        // [M][K] activations, row stride lda (elements)
+    const void* b;        // [N][K] weights (int8 or 16-bit), row stride K
+    const void* scales;   // [N][K/128] f32 or f16 (int8 kinds)
+    const float* bias;    // [N] or NULL
+    void* out;            // output (meaning per epilogue)
+    const float* resid;   // [M][N] f32 residual (RESID_GATE)
+    void* out2;           // V^T output (QKV)
+    LtxAda ada;           // RESID_GATE gate table
+    int M, N, K;
+    int lda;
+    int ldo;              // output row stride (elements)
+    int nsplit;           // QKV: first V column
+    int igate;            // RESID_GATE ada row
+    int gelu;             // STORE: apply GELU-tanh
+    int out_f32;          // STORE: 1 = f32 output, 0 = 16-bit output
+    int tiles_m, tiles_n; // grid geometry (filled by host)
+} LtxGemmArgs;
+
+// Full-row qk RMSNorm (weighted, over all 4096 channels) + optional split-half
+// RoPE, writing the head-major 16-bit layout [H][rows][HD] the attention reads.
+typedef struct {
+    const float* x;     // [rows][ldx] f32 pre-norm projections
+    const float* w;     // [D] norm weight (f32 copy of the bf16 tensor)
+    const float* cos;   // [rows][H][64] or NULL (no RoPE)
+    const float* sin;
+    void* y;            // [H][rows][HD]
+    int rows;
+    int ldx;
+} LtxQkNormArgs;
+
+// Blockwise online-softmax attention with per-(token, head) gate.
+// q, k: [H][L][HD] 16-bit; vt: [H][HD][Lkv] 16-bit; glog: [Lq][H] f32 gate
+// logits (gate = 2*sigmoid); out: [Lq][D] 16-bit merged heads.
+typedef struct {
+    const void* q;
+    const void* k;
+    const void* vt;
+    const float* glog;
+    void* out;
+    int lq, lkv;
+    float scale_log2;   // softmax scale * log2(e)
+    int q_tiles;        // ceil(lq / q-tile)
+} LtxAttnArgs;
+
+// Gate logits: glog[t][h] = a[t] . gw[h] + gb[h] (N = 32 heads).
+typedef struct {
+    const void* a;      // [M][D] 16-bit
+    const void* gw;     // [H][D] 16-bit
+    const float* gb;    // [H]
+    float* out;         // [M][H]
+    int M;
+} LtxGateArgs;
+
+// Dequantisation probe: out[n][k] = f32(q[n][k]) * scale[n][k/128], exactly
+// as the GEMM's in-register dequant computes it before the 16-bit rounding.
+typedef struct {
+    const int8_t* q;
+    const void* scales;
+    float* out32;       // f32 value
+    void* out16;        // the 16-bit MFMA operand
+    int N, K;
+    int scale_f16;
+} LtxDequantArgs;
+
+// f32 reference-precision kernels (mode LTX_MODE_F32).
+typedef struct {
+    const float* a;     // [M][K]
+    const void* b;      // int8 [N][K] or bf16 [N][K]
+    const void* scales;
+    int bkind;          // 0: int8+f32s, 1: int8+f16s, 2: bf16
+    const float* bias;
+    float* out;
+    const float* resid;
+    LtxAda ada;
+    int M, N, K;
+    int epi;            // LTX_EPI_STORE / RESID_GATE
+    int gelu;
+    int igate;
+} LtxGemm32Args;
+
+typedef struct {
+    const float* q;     // [Lq][D] (roped / normed)
+    const float* k;     // [Lkv][D]
+    const float* v;     // [Lkv][D]
+    const float* glog;  // [Lq][H]
+    float* out;         // [Lq][D]
+    int lq, lkv;
+    float scale;
+} LtxAttn32Args;
+
+typedef struct {
+    float* x;           // [rows][D] in place
+    const float* w;     // [D]
+    const float* cos;   // [rows][H][64] or NULL
+    const float* sin;
+    int rows;
+    int ldx;
+} LtxQkNorm32Args;
+
+#ifdef __cplusplus
+}
+#endif

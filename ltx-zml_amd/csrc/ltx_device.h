@@ -1,0 +1,106 @@
+// Device-side helpers shared by the gfx950 kernels: 16-bit operand traits,
+// MFMA wrappers, conversions, the AdaLN gather and block reductions.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "ltx_args.h"
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Operand traits: the MFMA operand type (f16 or bf16), its 8-wide vector,
+// f32 -> 16-bit rounding (round-to-nearest-even) and the 32x32x16 MFMA.
+template <typename T>
+struct Op;
+
+template <>
+struct Op<_Float16> {
+    typedef f16x8 v8;
+    static __device__ __forceinline__ uint16_t bits(float f) {
+        _Float16 h = (_Float16)f;
+        return __builtin_bit_cast(uint16_t, h);
+    }
+    static __device__ __forceinline__ float to_f32(uint16_t b) {
+        return (float)__builtin_bit_cast(_Float16, b);
+    }
+    static __device__ __forceinline__ f32x16 mfma32(v8 a, v8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Op<__bf16> {
+    typedef bf16x8 v8;
+    static __device__ __forceinline__ uint16_t bits(float f) {
+        __bf16 h = (__bf16)f;
+        return __builtin_bit_cast(uint16_t, h);
+    }
+    static __device__ __forceinline__ float to_f32(uint16_t b) {
+        return __builtin_bit_cast(float, (uint32_t)b << 16);
+    }
+    static __device__ __forceinline__ f32x16 mfma32(v8 a, v8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+// Pack two f32 into two 16-bit lanes of one dword (lo = a).
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return (uint32_t)Op<T>::bits(a) | ((uint32_t)Op<T>::bits(b) << 16);
+}
+
+// Dequantised 16-bit weight operands for two int8 values. u = q + 128 is the
+// byte read as unsigned (q ^ 0x80), nb = -128 s; fma(u, s, nb) is the exact
+// q * s rounded once to f32 — the dq4 value of ltx/block.zig:462-471. The
+// 16-bit operand is then: f16 — the compiler fuses fma + convert into
+// v_fma_mix, a single round-to-nearest-even of the exact q * s to f16; bf16 —
+// round-to-nearest-even of that f32 value. Shared by the GEMM staging path and
+// the dequantisation probe, so the probe reports exactly what the MFMA sees.
+template <typename T>
+__device__ __forceinline__ uint32_t deq_pack2(float u0, float u1, float s, float nb) {
+    return pack2<T>(__builtin_fmaf(u0, s, nb), __builtin_fmaf(u1, s, nb));
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+    return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+    return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// AdaLN value (ltx/block.zig:47-67): f32 add of the table row and the
+// timestep-table row selected by tidx.
+__device__ __forceinline__ float ada_val(const LtxAda& a, int t, int i, int c) {
+    int r = a.tidx[t];
+    return a.tstab[((size_t)r * 9 + i) * LTX_D + c] + a.sst[(size_t)i * LTX_D + c];
+}
+
+// Sum over a 256-thread block (4 waves). `red` holds 4 floats of LDS.
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float s = red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
+    return s;
+}
+
+// GELU, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))),
+// with tanh(u) = 1 - 2 / (exp(2u) + 1) (exact identity; saturates cleanly).
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float c = 0.7978845608028654f;
+    float u = c * (x + 0.044715f * x * x * x);
+    float e = __expf(2.0f * u);
+    float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+    return 0.5f * x * (1.0f + t);
+}
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + __expf(-x)); }

@@ -1,0 +1,91 @@
+"""Timestep conditioning: sigma -> the block's AdaLN inputs.
+
+The block consumes precomputed tables, tstab [K, 9, D] + tidx [T] and
+pts2 [2, D] (ltx/block.zig:47-67, ltx/e2e_prod.zig:243-246). They come from
+sigma through the model's adaln_single / prompt_adaln_single MLPs
+(ltx/core_parts.zig:42-49, 112-141):
+
+  sinusoid(t) = [cos(1000 t f), sin(1000 t f)],  f_k = exp(-ln(1e4) k / 128)
+  emb  = lin2(silu(lin1(sinusoid(t))))            (256 -> 4096 -> 4096)
+  ts9  = lin_out(silu(emb))                       (4096 -> 9 * 4096)
+  pts2 = p_out(silu(p_lin2(silu(p_lin1(sinusoid(sigma))))))   (-> 2 * 4096)
+
+Real checkpoint weights are unavailable offline, so the MLP weights are drawn
+here (seeded N(0, 0.02), rounded to bf16 like checkpoint tensors). Per-token
+timesteps are mask * sigma with the production pass's striped mask
+(ltx/e2e_prod.zig:218-229): mask 0 for the first T/7 tokens, 0.5 for the
+next T/7, 1 for the rest — K = 3 distinct rows gathered through tidx.
+"""
+from __future__ import annotations
+
+import zlib
+
+import numpy as np
+
+from .blockfmt import D, bf16_bits, bf16_to_f32
+
+TE, HALF = 256, 128
+
+
+def _rng(seed: int, name: str) -> np.random.Generator:
+    return np.random.default_rng([seed, zlib.crc32(name.encode())])
+
+
+def _w(seed: int, name: str, shape) -> np.ndarray:
+    return bf16_to_f32(bf16_bits(_rng(seed, name).standard_normal(shape, dtype=np.float32) * 0.02))
+
+
+def sinusoid(t: np.ndarray) -> np.ndarray:
+    """f32 sinusoid of t * 1000, cos half first (ltx/core_parts.zig:42-49)."""
+    t = np.asarray(t, dtype=np.float32).reshape(-1, 1)
+    freqs = np.exp(np.arange(HALF, dtype=np.float32) * np.float32(-np.log(1e4) / HALF)).astype(np.float32)
+    arg = (t * np.float32(1000.0)) * freqs[None, :]
+    return np.concatenate([np.cos(arg), np.sin(arg)], axis=1).astype(np.float32)
+
+
+def _silu(x):
+    return x / (1.0 + np.exp(-x))
+
+
+def _mlp_tables(seed: int):
+    w = {}
+    for pfx in ("ada", "pada"):
+        w[pfx + "_l1_w"] = _w(seed, pfx + "_l1_w", (D, TE))
+        w[pfx + "_l1_b"] = _w(seed, pfx + "_l1_b", (D,))
+        w[pfx + "_l2_w"] = _w(seed, pfx + "_l2_w", (D, D))
+        w[pfx + "_l2_b"] = _w(seed, pfx + "_l2_b", (D,))
+    w["ada_out_w"] = _w(seed, "ada_out_w", (9 * D, D))
+    w["ada_out_b"] = _w(seed, "ada_out_b", (9 * D,))
+    w["pada_out_w"] = _w(seed, "pada_out_w", (2 * D, D))
+    w["pada_out_b"] = _w(seed, "pada_out_b", (2 * D,))
+    return w
+
+
+_CACHE: dict = {}
+
+
+def tables(sigma: float, T: int, seed: int = 7, striped: bool = True):
+    """(tstab [K, 9, D] f32, tidx [T] i32, pts2 [2, D] f32) for noise level sigma."""
+    if seed not in _CACHE:
+        _CACHE[seed] = _mlp_tables(seed)
+    w = _CACHE[seed]
+    if striped:
+        mask = np.array([0.0, 0.5, 1.0], dtype=np.float32)
+        tidx = np.full(T, 2, dtype=np.int32)
+        tidx[: T // 7] = 0
+        tidx[T // 7: 2 * T // 7] = 1
+    else:
+        mask = np.array([1.0], dtype=np.float32)
+        tidx = np.zeros(T, dtype=np.int32)
+    t = (mask * np.float32(sigma)).astype(np.float32)
+    e = sinusoid(t)
+    h = _silu(e @ w["ada_l1_w"].T + w["ada_l1_b"])
+    emb = h @ w["ada_l2_w"].T + w["ada_l2_b"]
+    ts9 = _silu(emb) @ w["ada_out_w"].T + w["ada_out_b"]
+    tstab = np.ascontiguousarray(ts9.reshape(len(t), 9, D), dtype=np.float32)
+    ps = sinusoid(np.array([sigma], dtype=np.float32))
+    ph = _silu(ps @ w["pada_l1_w"].T + w["pada_l1_b"])
+    pe = ph @ w["pada_l2_w"].T + w["pada_l2_b"]
+    p2 = _silu(pe) @ w["pada_out_w"].T + w["pada_out_b"]
+    pts2 = np.ascontiguousarray(p2.reshape(2, D), dtype=np.float32)
+    return tstab, tidx, pts2

@@ -1,0 +1,245 @@
+"""ctypes bindings of libltx_amd.so (include/ltx_block.h, include/ltx_loader.h).
+
+Device memory and streams come from PyTorch (plumbing only); every compute
+call goes through the C ABI into the gfx950 kernels. There is no fallback:
+a missing library or a failed call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+
+import numpy as np
+
+from . import blockfmt as bf
+
+PKG_DIR = pathlib.Path(__file__).resolve().parent.parent
+LIB_PATH = PKG_DIR / "libltx_amd.so"
+
+MODE_F16, MODE_BF16, MODE_F32 = 0, 1, 2
+MODES = {"f16": MODE_F16, "bf16": MODE_BF16, "f32": MODE_F32}
+STAGES = ["norm_msa", "q1", "k1", "v1", "glog1", "attn1", "x_sa", "attn_in", "attn2", "x_ca", "ff_in", "ff_h"]
+
+W_COUNT, Q_COUNT = 28, 10
+
+_lib = None
+
+
+class LtxError(RuntimeError):
+    pass
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise LtxError(f"{LIB_PATH} is not built; run `python ltx-zml_amd/build.py`")
+    L = C.CDLL(str(LIB_PATH))
+    vp, i32, i64, u64 = C.c_void_p, C.c_int, C.c_int64, C.c_uint64
+    sig = {
+        "ltx_init": (i32, [i32, C.POINTER(vp)]),
+        "ltx_destroy": (None, [vp]),
+        "ltx_last_error": (C.c_char_p, [vp]),
+        "ltx_version": (C.c_char_p, []),
+        "ltx_block_weights_from_blob": (i32, [vp, vp, u64, C.c_char_p, i64, C.POINTER(vp)]),
+        "ltx_block_weights_from_host": (i32, [vp, C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), i32, C.POINTER(vp)]),
+        "ltx_block_weights_free": (None, [vp, vp]),
+        "ltx_block_weights_bytes": (u64, [vp]),
+        "ltx_block_forward": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, vp, vp, vp, i32, vp, i32, vp]),
+        "ltx_block_stage": (i32, [vp, i32, C.POINTER(vp), C.POINTER(u64)]),
+        "ltx_op_linear_q8": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
+        "ltx_op_attention": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
+        "ltx_op_dequant": (i32, [vp, vp, vp, i32, i32, i32, vp, vp, i32, vp]),
+        "ltx_rope_tables": (i32, [vp, i32, vp, vp, i32]),
+        "ltx_profile_enable": (i32, [vp, i32]),
+        "ltx_profile_read": (i32, [vp, C.c_char_p, C.POINTER(C.c_double), C.POINTER(i32)]),
+        "ltx_profile_reset": (i32, [vp]),
+        "ltx_blob_open": (i32, [C.c_char_p, C.POINTER(vp)]),
+        "ltx_blob_close": (None, [vp]),
+        "ltx_blob_check_layout": (i32, [vp]),
+        "ltx_blob_verify": (i32, [vp]),
+        "ltx_blob_data": (vp, [vp, C.POINTER(u64)]),
+        "ltx_blob_manifest_text": (C.c_char_p, [vp]),
+        "ltx_blob_block_index": (i64, [vp]),
+        "ltx_blob_find": (i32, [vp, C.c_char_p, C.POINTER(u64), C.POINTER(u64), C.c_char_p, i32]),
+        "ltx_ring_create": (i32, [C.POINTER(vp), i32, C.POINTER(i32), i32, i32, u64, i32, C.POINTER(vp)]),
+        "ltx_ring_static_check": (i32, [vp]),
+        "ltx_ring_start": (i32, [vp]),
+        "ltx_ring_acquire": (i32, [vp, i32, C.POINTER(vp), C.POINTER(u64)]),
+        "ltx_ring_release": (i32, [vp, i32]),
+        "ltx_ring_abort": (None, [vp]),
+        "ltx_ring_stats": (i32, [vp, C.POINTER(u64), C.POINTER(u64), C.POINTER(u64), C.POINTER(u64)]),
+        "ltx_ring_set_reader_delay_us": (i32, [vp, C.c_uint32]),
+        "ltx_ring_destroy": (None, [vp]),
+        "ltx_loader_last_error": (C.c_char_p, []),
+        "ltx_sha256_hex": (i32, [vp, u64, C.c_char_p]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L
+    return L
+
+
+def _ptr(t) -> int | None:
+    """Device/host address of a torch tensor or numpy array (None -> NULL)."""
+    if t is None:
+        return None
+    if isinstance(t, np.ndarray):
+        return t.ctypes.data
+    return t.data_ptr()
+
+
+def rope_tables(grid: np.ndarray, graph_layout: bool = True) -> tuple[np.ndarray, np.ndarray]:
+    """Host f64 3D-RoPE tables (ltx/block_conformance.zig:87-126)."""
+    grid = np.ascontiguousarray(grid, dtype=np.float32)
+    T = grid.shape[1]
+    shape = (T, 32, 64) if graph_layout else (32, T, 64)
+    cos, sin = np.empty(shape, np.float32), np.empty(shape, np.float32)
+    if not lib().ltx_rope_tables(_ptr(grid), T, _ptr(cos), _ptr(sin), int(graph_layout)):
+        raise LtxError(lib().ltx_last_error(None).decode())
+    return cos, sin
+
+
+def sha256_hex(data: bytes) -> str:
+    out = C.create_string_buffer(65)
+    lib().ltx_sha256_hex(data, len(data), out)
+    return out.value.decode()
+
+
+class Weights:
+    def __init__(self, ctx: "Context", handle: int):
+        self.ctx, self.handle = ctx, handle
+
+    @property
+    def nbytes(self) -> int:
+        return lib().ltx_block_weights_bytes(self.handle)
+
+    def free(self):
+        if self.handle:
+            lib().ltx_block_weights_free(self.ctx.handle, self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Context:
+    """One device context (ltx_init). Not thread-safe."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        if not lib().ltx_init(device, C.byref(h)):
+            raise LtxError("ltx_init: " + lib().ltx_last_error(None).decode())
+        self.handle = h.value
+        self.device = device
+
+    def _check(self, ok: int, what: str):
+        if not ok:
+            raise LtxError(f"{what}: " + lib().ltx_last_error(self.handle).decode())
+
+    def close(self):
+        if self.handle:
+            lib().ltx_destroy(self.handle)
+            self.handle = None
+
+    # ---- weights ----
+    def upload(self, bt: bf.BlockTensors) -> Weights:
+        base = (C.c_void_p * W_COUNT)()
+        for i, f in enumerate(bf.FIELDS):
+            base[i] = bt.base[f].ctypes.data
+        q8 = (C.c_void_p * Q_COUNT)()
+        q8s = (C.c_void_p * Q_COUNT)()
+        for i, qn in enumerate(bf.Q8_FIELDS):
+            if qn in bt.q8:
+                q8[i] = bt.q8[qn].ctypes.data
+                q8s[i] = bt.q8s[qn].ctypes.data
+        h = C.c_void_p()
+        self._check(lib().ltx_block_weights_from_host(self.handle, base, q8, q8s, int(bt.scale_f16), C.byref(h)),
+                    "ltx_block_weights_from_host")
+        return Weights(self, h.value)
+
+    def upload_blob(self, blob: bytes | np.ndarray, manifest_json: str, block: int) -> Weights:
+        buf = np.frombuffer(blob, dtype=np.uint8) if not isinstance(blob, np.ndarray) else blob
+        h = C.c_void_p()
+        self._check(lib().ltx_block_weights_from_blob(self.handle, buf.ctypes.data, buf.nbytes,
+                                                      manifest_json.encode(), block, C.byref(h)),
+                    "ltx_block_weights_from_blob")
+        return Weights(self, h.value)
+
+    # ---- forward ----
+    def forward(self, w: Weights, x, tstab, tidx, ctx, pts2, cos, sin, y, mode: int = MODE_F16, stream=None):
+        T, S, K = x.shape[0], ctx.shape[0], tstab.shape[0]
+        st = stream.cuda_stream if stream is not None else _current_stream()
+        self._check(lib().ltx_block_forward(self.handle, w.handle, _ptr(x), _ptr(tstab), K, _ptr(tidx), _ptr(ctx), S,
+                                            _ptr(pts2), _ptr(cos), _ptr(sin), T, _ptr(y), mode, st),
+                    "ltx_block_forward")
+        return y
+
+    def stage(self, name: str):
+        import torch
+        p, n = C.c_void_p(), C.c_uint64()
+        self._check(lib().ltx_block_stage(self.handle, STAGES.index(name), C.byref(p), C.byref(n)), "ltx_block_stage")
+        out = torch.empty(n.value, dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+        _memcpy_dtod(out.data_ptr(), p.value, n.value)
+        return out
+
+    # ---- operators ----
+    def linear_q8(self, a, q, s, bias, y, mode=MODE_F16, gelu=False, stream=None):
+        M, K = a.shape
+        N = q.shape[0]
+        import torch
+        st = stream.cuda_stream if stream is not None else _current_stream()
+        self._check(lib().ltx_op_linear_q8(self.handle, _ptr(a), _ptr(q), _ptr(s), int(s.dtype == torch.float16),
+                                           _ptr(bias), _ptr(y), int(y.dtype == torch.float32), M, N, K, int(gelu),
+                                           mode, st), "ltx_op_linear_q8")
+        return y
+
+    def attention(self, q, k, v, glog, out, lq, lkv, mode=MODE_F16, stream=None):
+        st = stream.cuda_stream if stream is not None else _current_stream()
+        self._check(lib().ltx_op_attention(self.handle, _ptr(q), _ptr(k), _ptr(v), _ptr(glog), _ptr(out), lq, lkv,
+                                           mode, st), "ltx_op_attention")
+        return out
+
+    def dequant(self, q, s, out32, out16, mode=MODE_F16, stream=None):
+        import torch
+        N, K = q.shape
+        st = stream.cuda_stream if stream is not None else _current_stream()
+        self._check(lib().ltx_op_dequant(self.handle, _ptr(q), _ptr(s), int(s.dtype == torch.float16), N, K,
+                                         _ptr(out32), _ptr(out16), mode, st), "ltx_op_dequant")
+
+    # ---- profiling ----
+    def profile(self, enable: bool):
+        self._check(lib().ltx_profile_enable(self.handle, int(enable)), "ltx_profile_enable")
+
+    def profile_reset(self):
+        self._check(lib().ltx_profile_reset(self.handle), "ltx_profile_reset")
+
+    def profile_read(self, substr: str = "") -> tuple[float, int]:
+        ms, n = C.c_double(), C.c_int()
+        self._check(lib().ltx_profile_read(self.handle, substr.encode(), C.byref(ms), C.byref(n)), "ltx_profile_read")
+        return ms.value, n.value
+
+
+def _current_stream() -> int:
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _memcpy_dtod(dst: int, src: int, n: int):
+    import torch
+    # a uint8 view of the source allocation through torch's storage API is not
+    # available for foreign pointers; use hipMemcpy from the HIP runtime.
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    hip.hipMemcpy.restype = C.c_int
+    rc = hip.hipMemcpy(dst, src, n, 3)  # hipMemcpyDeviceToDevice
+    if rc != 0:
+        raise LtxError(f"hipMemcpy failed ({rc})")
+    torch.cuda.synchronize()

@@ -1,0 +1,273 @@
+"""The oracle — TEST INFRASTRUCTURE ONLY.
+
+A CPU restatement of the reference's block forward (QBlock.qBlockOutAll,
+ltx/block.zig:544-574, with the blockwise attention of ltx/block.zig:105-154)
+and of its host contracts (RoPE tables ltx/block_conformance.zig:87-126, the
+int8-g128 quantizer tools/quantize_block.py:51-59, dq4 ltx/block.zig:462-471).
+Only tests, the smoke check and the benchmark's CPU-baseline leg may use it,
+and only as the checker / baseline; the product never imports it.
+
+Two layers:
+- ``ltx_oracle.c`` (built by ``oracle/build.py``): f64 parity oracle and the
+  f32 CPU-baseline build of the same source;
+- the numpy restatements below, written independently of the C code, used to
+  pin it (``rope_tables_np``, ``quantize_np``, ``sdpa_np``, ``block_np``).
+
+Parity status of each function is documented where it is pinned (tests/).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+D, H, HD, FF = 4096, 32, 128, 16384
+NF = 682
+MAXPOS = (20.0, 2048.0, 2048.0)
+ST_NAMES = ["s1_norm_msa", "q1_roped", "k1_roped", "v1", "attn1_merged", "s3_attn1", "s4_after_sa", "s4_normed",
+            "attn_in", "enc", "q2_normed", "k2_normed", "v2", "attn2_merged", "s5_ca_out", "x_ca", "s6_ff_in",
+            "ff_h", "s7_ff_out"]
+BASE_ORDER = ["q1_w", "q1_b", "k1_w", "k1_b", "v1_w", "v1_b", "o1_w", "o1_b", "qn1", "kn1", "g1_w", "g1_b",
+              "q2_w", "q2_b", "k2_w", "k2_b", "v2_w", "v2_b", "o2_w", "o2_b", "qn2", "kn2", "g2_w", "g2_b",
+              "ff1_w", "ff2_w", "sst", "psst"]
+Q_ORDER = ["q1", "k1", "v1", "q2", "k2", "v2", "f1", "f2", "o1", "o2"]
+
+_libs: dict = {}
+
+
+def lib(real: str = "f64") -> C.CDLL:
+    if real in _libs:
+        return _libs[real]
+    p = HERE / "_build" / f"liboracle_{real}.so"
+    if not p.exists():
+        raise RuntimeError(f"{p} not built; run `python oracle/build.py`")
+    L = C.CDLL(str(p))
+    vp, i32 = C.c_void_p, C.c_int
+    L.orc_block_forward.restype = i32
+    L.orc_block_forward.argtypes = [C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), i32, vp, vp, i32, vp, vp, i32, vp,
+                                    vp, vp, i32, i32, i32, vp, C.POINTER(vp)]
+    L.orc_rope_tables.argtypes = [vp, i32, vp, vp]
+    L.orc_rope_freqs.argtypes = [vp]
+    L.orc_quantize.argtypes = [vp, i32, i32, i32, i32, vp, vp]
+    L.orc_dequant.argtypes = [vp, vp, i32, i32, i32, vp]
+    L.orc_sdpa.argtypes = [vp, i32, vp, vp, i32, i32, vp]
+    L.orc_sdpa.restype = i32
+    L.orc_linear.argtypes = [vp, i32, i32, vp, vp, vp, i32, vp, i32, vp]
+    L.orc_rms.argtypes = [vp, i32, i32, vp, vp]
+    _libs[real] = L
+    return L
+
+
+def _rdt(real):
+    return np.float64 if real == "f64" else np.float32
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+# ---- C oracle wrappers ------------------------------------------------------
+
+def rope_tables(grid: np.ndarray):
+    """Bundle layout [H][T][64] cos, sin (f32)."""
+    grid = np.ascontiguousarray(grid, np.float32)
+    T = grid.shape[1]
+    cos, sin = np.empty((H, T, 64), np.float32), np.empty((H, T, 64), np.float32)
+    lib().orc_rope_tables(grid.ctypes.data, T, cos.ctypes.data, sin.ctypes.data)
+    return cos, sin
+
+
+def rope_freqs() -> np.ndarray:
+    f = np.empty(NF, np.float64)
+    lib().orc_rope_freqs(f.ctypes.data)
+    return f
+
+
+def quantize(w_bf16: np.ndarray, gs: int = 128, bits: int = 8):
+    w_bf16 = np.ascontiguousarray(w_bf16, np.uint16)
+    O, I = w_bf16.shape
+    q, s = np.empty((O, I), np.int8), np.empty((O, I // gs), np.float32)
+    lib().orc_quantize(w_bf16.ctypes.data, O, I, gs, bits, q.ctypes.data, s.ctypes.data)
+    return q, s
+
+
+def dequant(q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.int8)
+    s = np.ascontiguousarray(s)
+    out = np.empty(q.shape, np.float32)
+    lib().orc_dequant(q.ctypes.data, s.ctypes.data, int(s.dtype == np.float16), q.shape[0], q.shape[1],
+                      out.ctypes.data)
+    return out
+
+
+def sdpa(q, k, v, chunk: int, real: str = "f64"):
+    """q [Lq, D], k/v [Lkv, D] -> [Lq, D]; chunk 0 = dense softmax."""
+    dt = _rdt(real)
+    q, k, v = (np.ascontiguousarray(a, dt) for a in (q, k, v))
+    out = np.empty_like(q)
+    if not lib(real).orc_sdpa(q.ctypes.data, q.shape[0], k.ctypes.data, v.ctypes.data, k.shape[0], chunk,
+                              out.ctypes.data):
+        raise ValueError(f"chunk {chunk} does not divide the key count {k.shape[0]}")
+    return out
+
+
+def linear(x, w_bf16=None, q=None, s=None, b_bf16=None, real: str = "f64"):
+    dt = _rdt(real)
+    x = np.ascontiguousarray(x, dt)
+    M, K = x.shape
+    N = (q if q is not None else w_bf16).shape[0]
+    y = np.empty((M, N), dt)
+    sf16 = int(s is not None and s.dtype == np.float16)
+    lib(real).orc_linear(x.ctypes.data, M, K, _p(w_bf16), _p(q), _p(s), sf16, _p(b_bf16), N, y.ctypes.data)
+    return y
+
+
+def block_forward(bt, inp: dict, cos_thf: np.ndarray, sin_thf: np.ndarray, chunk: int = 16, cross_chunk: int = 0,
+                  real: str = "f64", stages: bool = False, threads: int | None = None):
+    """QBlock.qBlockOutAll on the CPU. ``bt`` is a BlockTensors (numpy),
+    ``inp`` holds x, ctx, tstab, tidx, pts2; cos/sin in graph layout [T][H][64]."""
+    L = lib(real)
+    dt = _rdt(real)
+    base = (C.c_void_p * 28)(*[bt.base[f].ctypes.data for f in BASE_ORDER])
+    q8 = (C.c_void_p * 10)(*[bt.q8[n].ctypes.data if n in bt.q8 else None for n in Q_ORDER])
+    q8s = (C.c_void_p * 10)(*[bt.q8s[n].ctypes.data if n in bt.q8s else None for n in Q_ORDER])
+    x = np.ascontiguousarray(inp["x"], np.float32)
+    T, S = x.shape[0], inp["ctx"].shape[0]
+    out = np.empty((T, D), dt)
+    st_bufs = {}
+    st_arr = None
+    if stages:
+        shapes = {"ff_h": (T, FF), "enc": (S, D), "k2_normed": (S, D), "v2": (S, D)}
+        st_bufs = {n: np.empty(shapes.get(n, (T, D)), dt) for n in ST_NAMES}
+        st_arr = (C.c_void_p * len(ST_NAMES))(*[st_bufs[n].ctypes.data for n in ST_NAMES])
+    tstab = np.ascontiguousarray(inp["tstab"], np.float32)
+    tidx = np.ascontiguousarray(inp["tidx"], np.int32)
+    ctx = np.ascontiguousarray(inp["ctx"], np.float32)
+    pts2 = np.ascontiguousarray(inp["pts2"], np.float32)
+    cos_thf = np.ascontiguousarray(cos_thf, np.float32)
+    sin_thf = np.ascontiguousarray(sin_thf, np.float32)
+    ok = L.orc_block_forward(base, q8, q8s, int(bt.scale_f16), x.ctypes.data, tstab.ctypes.data, tstab.shape[0],
+                             tidx.ctypes.data, ctx.ctypes.data, S, pts2.ctypes.data, cos_thf.ctypes.data,
+                             sin_thf.ctypes.data, T, chunk, cross_chunk, out.ctypes.data, st_arr)
+    if not ok:
+        raise RuntimeError("oracle block forward failed")
+    return (out, st_bufs) if stages else out
+
+
+# ---- numpy restatements (independent of the C code) -----------------------
+
+def rope_freqs_np() -> np.ndarray:
+    """theta ** linspace(0, 1, 682) * pi / 2 in f64, rounded to f32."""
+    return (10000.0 ** np.linspace(0.0, 1.0, NF, dtype=np.float64) * np.pi / 2).astype(np.float32).astype(np.float64)
+
+
+def rope_tables_np(grid: np.ndarray):
+    """precompute_freqs_cis(SPLIT) semantics, numpy f64: [H][T][64] f32."""
+    g = np.asarray(grid, np.float64)  # [3, T, 2]
+    mid = (g[..., 0] + g[..., 1]) / 2.0  # [3, T]
+    frac = mid / np.array(MAXPOS)[:, None]
+    arg = frac * 2.0 - 1.0  # [3, T]
+    f = rope_freqs_np()  # [NF]
+    th = f[None, :, None] * arg.T[:, None, :]  # [T, NF, 3]
+    th = th.reshape(th.shape[0], NF * 3)  # axis triplets adjacent, freq-major
+    cos = np.concatenate([np.ones((th.shape[0], 2)), np.cos(th)], axis=1)
+    sin = np.concatenate([np.zeros((th.shape[0], 2)), np.sin(th)], axis=1)
+    T = th.shape[0]
+    cos = cos.reshape(T, H, 64).transpose(1, 0, 2).astype(np.float32)
+    sin = sin.reshape(T, H, 64).transpose(1, 0, 2).astype(np.float32)
+    return np.ascontiguousarray(cos), np.ascontiguousarray(sin)
+
+
+def quantize_np(w_bf16: np.ndarray, gs: int = 128, bits: int = 8):
+    qmax, lo = (7, -8) if bits == 4 else (127, -128)
+    w = (np.asarray(w_bf16, np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    o, i = w.shape
+    wg = w.reshape(o, i // gs, gs)
+    am = np.abs(wg).max(axis=2, keepdims=True)
+    sc = np.where(am > 0, am / qmax, 1.0)
+    q = np.clip(np.round(wg / sc), lo, qmax).astype(np.int8).reshape(o, i)
+    return q, sc.squeeze(2).astype(np.float32)
+
+
+def sdpa_np(q, k, v):
+    """Dense softmax attention, f64, K scaled by f32(1/sqrt(128))."""
+    q, k, v = (np.asarray(a, np.float64) for a in (q, k, v))
+    Lq, Lk = q.shape[0], k.shape[0]
+    qh = q.reshape(Lq, H, HD).transpose(1, 0, 2)
+    kh = k.reshape(Lk, H, HD).transpose(1, 0, 2) * float(np.float32(1.0) / np.sqrt(np.float32(128.0)))
+    vh = v.reshape(Lk, H, HD).transpose(1, 0, 2)
+    s = qh @ kh.transpose(0, 2, 1)
+    s = np.exp(s - s.max(-1, keepdims=True))
+    o = (s / s.sum(-1, keepdims=True)) @ vh
+    return o.transpose(1, 0, 2).reshape(Lq, D)
+
+
+def _bf(b):
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def block_np(bt, inp: dict, cos_thf, sin_thf):
+    """Dense-attention numpy restatement of qBlockOutAll (f64)."""
+    W = {}
+    for f in BASE_ORDER[:-2]:
+        W[f] = _bf(bt.base[f])
+    for n, wf in {"q1": "q1_w", "k1": "k1_w", "v1": "v1_w", "q2": "q2_w", "k2": "k2_w", "v2": "v2_w",
+                  "f1": "ff1_w", "f2": "ff2_w", "o1": "o1_w", "o2": "o2_w"}.items():
+        if n in bt.q8:
+            q = bt.q8[n].astype(np.float32)
+            s = bt.q8s[n].astype(np.float32)
+            W[wf] = (q.reshape(q.shape[0], -1, 128) * s[:, :, None]).reshape(q.shape).astype(np.float64)
+    sst = bt.base["sst"].astype(np.float64)
+    psst = bt.base["psst"].astype(np.float64)
+    x = inp["x"].astype(np.float64)
+    ctx = inp["ctx"].astype(np.float64)
+    tab = inp["tstab"].astype(np.float64)[inp["tidx"]]  # [T, 9, D]
+    ada = [tab[:, i, :] + sst[i] for i in range(9)]
+    cs, sn = cos_thf.astype(np.float64), sin_thf.astype(np.float64)
+
+    def rms(a, w=None):
+        r = a / np.sqrt((a * a).mean(-1, keepdims=True) + 1e-6)
+        return r * w if w is not None else r
+
+    def rope(a):
+        T = a.shape[0]
+        a4 = a.reshape(T, H, 2, 64)
+        u, v = a4[:, :, 0], a4[:, :, 1]
+        return np.concatenate([u * cs - v * sn, v * cs + u * sn], -1).reshape(T, D)
+
+    def attn(xq, xkv, p, use_rope):
+        q = rms(xq @ W[p + "q_w"].T + W[p + "q_b"], W["qn" + p[-1]])
+        k = rms(xkv @ W[p + "k_w"].T + W[p + "k_b"], W["kn" + p[-1]])
+        v = xkv @ W[p + "v_w"].T + W[p + "v_b"]
+        if use_rope:
+            q, k = rope(q), rope(k)
+        o = sdpa_np(q, k, v)
+        g = 2.0 / (1.0 + np.exp(-(xq @ W["g" + p[-1] + "_w"].T + W["g" + p[-1] + "_b"])))
+        o = (o.reshape(-1, H, HD) * g[:, :, None]).reshape(-1, D)
+        return o @ W[p + "o_w"].T + W[p + "o_b"]
+
+    # weight names in W use q1_w etc.; adapt the prefix scheme
+    W2 = {}
+    for a in ("1", "2"):
+        for t in ("q", "k", "v", "o"):
+            W2[f"a{a}{t}_w"] = W[f"{t}{a}_w"]
+            W2[f"a{a}{t}_b"] = W[f"{t}{a}_b"]
+    W.update(W2)
+    n = rms(x) * (1 + ada[1]) + ada[0]
+    x_sa = x + attn(n, n, "a1", True) * ada[2]
+    ai = rms(x_sa) * (1 + ada[7]) + ada[6]
+    kv = psst + inp["pts2"].astype(np.float64)
+    enc = ctx * (1 + kv[1]) + kv[0]
+    x_ca = x_sa + attn(ai, enc, "a2", False) * ada[8]
+    fi = rms(x_ca) * (1 + ada[4]) + ada[3]
+    h = fi @ W["ff1_w"].T
+    h = 0.5 * h * (1 + np.tanh(np.sqrt(2 / np.pi) * (h + 0.044715 * h ** 3)))
+    return x_ca + (h @ W["ff2_w"].T) * ada[5]
+
+
+def rel_rms(got, want) -> float:
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.sqrt(((got - want) ** 2).sum() / ((want ** 2).sum() + 1e-300)))

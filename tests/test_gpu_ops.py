@@ -1,0 +1,191 @@
+"""GPU parity of the isolated operators against the oracle, through the C ABI.
+
+Tolerances (rel-RMS):
+  dequant                     bit-exact (f32 value) / bit-exact RNE to 16-bit
+  GEMM vs oracle on the SAME 16-bit operands          <= 1e-5 (accumulation order only)
+  GEMM vs exact-weight oracle   f16 <= 1e-3, bf16 <= 6e-3 (one 16-bit rounding of q*s)
+  GEMM f32 mode                 <= 1e-5
+  attention vs dense f64 oracle on the same 16-bit Q/K/V:  f16 <= 2e-3, bf16 <= 1e-2, f32 <= 1e-5
+"""
+import numpy as np
+import pytest
+
+from conftest import say
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+import oracle  # noqa: E402
+from ltx_amd import blockfmt as bf  # noqa: E402
+from ltx_amd import runtime as rt  # noqa: E402
+
+MODES = {"f16": (rt.MODE_F16, torch.float16), "bf16": (rt.MODE_BF16, torch.bfloat16)}
+
+
+def to16(a: np.ndarray, dt):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dt)
+
+
+def f64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("scale_f16", [0, 1])
+@pytest.mark.parametrize("mode", ["f16", "bf16"])
+def test_dequant_bit_exact(ctx, mode, scale_f16):
+    say(f"dequant probe mode={mode} scale_f16={scale_f16}")
+    rng = np.random.default_rng(3)
+    N, K = 256, 512
+    q = np.stack([rng.permutation(np.arange(-128, 128, dtype=np.int16)) for _ in range(N * K // 256)])
+    q = q.reshape(N, K).astype(np.int8)
+    s = (10.0 ** rng.uniform(-6, 0, size=(N, K // 128))).astype(np.float32)
+    s[0, 0], s[1, 1], s[2, 0] = 1.0, 2.0 ** -20, 0.5
+    if scale_f16:
+        s = s.astype(np.float16)
+    want32 = oracle.dequant(q, s)
+    m, dt = MODES[mode]
+    dq, ds = torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda()
+    out32 = torch.empty((N, K), dtype=torch.float32, device="cuda")
+    out16 = torch.empty((N, K), dtype=dt, device="cuda")
+    ctx.dequant(dq, ds, out32, out16, mode=m)
+    torch.cuda.synchronize()
+    got32 = out32.cpu().numpy()
+    assert np.array_equal(got32.view(np.uint32), want32.view(np.uint32))
+    got16 = out16.cpu().view(torch.int16).numpy().view(np.uint16)
+    # f16: one round-to-nearest-even of the exact q * s (the fused FMA of the
+    # staging path; q * s is exact in f64); bf16: RNE of the f32 value.
+    exact = q.astype(np.float64) * np.repeat(s.astype(np.float64), 128, axis=1)
+    want16 = exact.astype(np.float16).view(np.uint16) if mode == "f16" else bf.bf16_bits(want32)
+    assert np.array_equal(got16, want16)
+
+
+def _gemm_case(M, N, K, seed, scale_f16=False, t3=True):
+    rng = np.random.default_rng(seed)
+    w = rng.standard_t(3, size=(N, K)) * 0.02 if t3 else rng.standard_normal((N, K)) * 0.02
+    q, s = bf.quantize_g128(bf.bf16_bits(w.astype(np.float32)))
+    if scale_f16:
+        s = s.astype(np.float16)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    return a, q, s, b
+
+
+@pytest.mark.parametrize("mode", ["f16", "bf16"])
+@pytest.mark.parametrize("M,N,K,gelu,out_f32,scale_f16", [
+    (256, 512, 4096, False, True, False),
+    (300, 256, 4096, True, False, False),   # ragged M, GELU, 16-bit output
+    (64, 768, 16384, False, True, True),    # long K, f16 scales
+    (512, 1024, 1024, False, False, False),
+])
+def test_linear_q8(ctx, mode, M, N, K, gelu, out_f32, scale_f16):
+    say(f"linear_q8 mode={mode} M={M} N={N} K={K} gelu={gelu} out_f32={out_f32} scale_f16={scale_f16}")
+    m, dt = MODES[mode]
+    a, q, s, b = _gemm_case(M, N, K, seed=M + N + K, scale_f16=scale_f16)
+    da = to16(a, dt).cuda()
+    dq, ds = torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda()
+    db = torch.from_numpy(b).cuda()
+    y = torch.empty((M, N), dtype=torch.float32 if out_f32 else dt, device="cuda")
+    ctx.linear_q8(da, dq, ds, db, y, mode=m, gelu=gelu)
+    # the 16-bit weight operand, as the GEMM stages it
+    w32 = torch.empty((N, K), dtype=torch.float32, device="cuda")
+    w16 = torch.empty((N, K), dtype=dt, device="cuda")
+    ctx.dequant(dq, ds, w32, w16, mode=m)
+    torch.cuda.synchronize()
+    a64 = f64(da)
+
+    def post(z):
+        z = z + b
+        return 0.5 * z * (1 + np.tanh(np.sqrt(2 / np.pi) * (z + 0.044715 * z ** 3))) if gelu else z
+
+    same_ops = post(a64 @ f64(w16).T)
+    exact_w = post(a64 @ oracle.dequant(q, s).astype(np.float64).T)
+    got = f64(y)
+    tol_same = 1e-5 if out_f32 else (1e-3 if mode == "f16" else 6e-3)
+    assert oracle.rel_rms(got, same_ops) <= tol_same
+    assert oracle.rel_rms(got, exact_w) <= (1e-3 if mode == "f16" else 6e-3)
+
+
+def test_linear_q8_f32_mode(ctx):
+    say("linear_q8 mode=f32 M=200 N=384 K=2048")
+    a, q, s, b = _gemm_case(200, 384, 2048, seed=5)
+    y = torch.empty((200, 384), dtype=torch.float32, device="cuda")
+    ctx.linear_q8(torch.from_numpy(a).cuda(), torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(),
+                  torch.from_numpy(b).cuda(), y, mode=rt.MODE_F32)
+    torch.cuda.synchronize()
+    want = oracle.linear(a, q=q, s=s) + b
+    assert oracle.rel_rms(f64(y), want) <= 1e-6
+
+
+def _heads(x, L):  # [L, D] -> [H, L, 128]
+    return np.ascontiguousarray(x.reshape(L, 32, 128).transpose(1, 0, 2))
+
+
+@pytest.mark.parametrize("mode", ["f16", "bf16"])
+@pytest.mark.parametrize("lq,lkv,gated", [(256, 256, True), (300, 200, True), (256, 32, False), (512, 1024, True),
+                                          (64, 77, True)])
+def test_attention(ctx, mode, lq, lkv, gated):
+    say(f"attention mode={mode} lq={lq} lkv={lkv} gated={gated}")
+    m, dt = MODES[mode]
+    rng = np.random.default_rng(lq * 7 + lkv)
+    q = rng.standard_normal((lq, 4096)).astype(np.float32)
+    k = rng.standard_normal((lkv, 4096)).astype(np.float32)
+    v = rng.standard_normal((lkv, 4096)).astype(np.float32)
+    glog = rng.standard_normal((lq, 32)).astype(np.float32) if gated else None
+    dq = to16(_heads(q, lq), dt).cuda()
+    dk = to16(_heads(k, lkv), dt).cuda()
+    dv = to16(np.ascontiguousarray(v.reshape(lkv, 32, 128).transpose(1, 2, 0)), dt).cuda()  # [H][128][L]
+    dg = torch.from_numpy(glog).cuda() if gated else None
+    out = torch.empty((lq, 4096), dtype=dt, device="cuda")
+    ctx.attention(dq, dk, dv, dg, out, lq, lkv, mode=m)
+    torch.cuda.synchronize()
+    q64 = f64(dq).transpose(1, 0, 2).reshape(lq, 4096)
+    k64 = f64(dk).transpose(1, 0, 2).reshape(lkv, 4096)
+    v64 = f64(dv).transpose(2, 0, 1).reshape(lkv, 4096)
+    want = oracle.sdpa(q64, k64, v64, chunk=0)
+    if gated:
+        g = 2.0 / (1.0 + np.exp(-glog.astype(np.float64)))
+        want = (want.reshape(lq, 32, 128) * g[:, :, None]).reshape(lq, 4096)
+    assert oracle.rel_rms(f64(out), want) <= (2e-3 if mode == "f16" else 1e-2)
+
+
+def test_attention_f32_mode(ctx):
+    say("attention mode=f32 lq=130 lkv=70")
+    rng = np.random.default_rng(11)
+    lq, lkv = 130, 70
+    q, k, v = (rng.standard_normal((n, 4096)).astype(np.float32) for n in (lq, lkv, lkv))
+    glog = rng.standard_normal((lq, 32)).astype(np.float32)
+    out = torch.empty((lq, 4096), dtype=torch.float32, device="cuda")
+    ctx.attention(*(torch.from_numpy(a).cuda() for a in (q, k, v)), torch.from_numpy(glog).cuda(), out, lq, lkv,
+                  mode=rt.MODE_F32)
+    torch.cuda.synchronize()
+    want = oracle.sdpa(q, k, v, chunk=0)
+    g = 2.0 / (1.0 + np.exp(-glog.astype(np.float64)))
+    want = (want.reshape(lq, 32, 128) * g[:, :, None]).reshape(lq, 4096)
+    assert oracle.rel_rms(f64(out), want) <= 1e-5
+
+
+def test_attention_special_cases(ctx):
+    """Identical keys -> mean of V; one dominant key -> that V row."""
+    say("attention special cases f16")
+    rng = np.random.default_rng(12)
+    lq, lkv = 64, 96
+    q = rng.standard_normal((lq, 4096)).astype(np.float32)
+    k = np.tile(rng.standard_normal((1, 4096)).astype(np.float32), (lkv, 1))
+    v = rng.standard_normal((lkv, 4096)).astype(np.float32)
+    dt = torch.float16
+    args = [to16(_heads(q, lq), dt).cuda(), to16(_heads(k, lkv), dt).cuda(),
+            to16(np.ascontiguousarray(v.reshape(lkv, 32, 128).transpose(1, 2, 0)), dt).cuda()]
+    out = torch.empty((lq, 4096), dtype=dt, device="cuda")
+    ctx.attention(*args, None, out, lq, lkv, mode=rt.MODE_F16)
+    torch.cuda.synchronize()
+    vm = f64(args[2]).transpose(2, 0, 1).reshape(lkv, 4096).mean(0)
+    assert np.abs(f64(out) - vm[None, :]).max() < 2e-3
+    # dominant key: key 37 equals 8 * q-direction for every head -> softmax ~ one-hot
+    k2 = rng.standard_normal((lkv, 4096)).astype(np.float32) * 0.01
+    qq = np.tile(rng.standard_normal((1, 4096)).astype(np.float32), (lq, 1))
+    k2[37] = qq[0] * 4.0
+    args2 = [to16(_heads(qq, lq), dt).cuda(), to16(_heads(k2, lkv), dt).cuda(), args[2]]
+    ctx.attention(*args2, None, out, lq, lkv, mode=rt.MODE_F16)
+    torch.cuda.synchronize()
+    v37 = f64(args[2]).transpose(2, 0, 1).reshape(lkv, 4096)[37]
+    assert np.abs(f64(out) - v37[None, :]).max() < 5e-3
