@@ -150,7 +150,14 @@ def pack(bt: BlockTensors, repo: str = "synthetic", revision: str = "synthetic",
         entries.append((name + "::q8", np.ascontiguousarray(q).tobytes(), "I8", [o, i]))
         entries.append((name + "::q8scale", np.ascontiguousarray(s).tobytes(),
                         "F16" if s.dtype == np.float16 else "F32", [o, i // GROUP]))
-    entries.sort(key=lambda t: t[0])
+    return pack_entries(entries, bt.block, repo, revision, source_file, model_version, packer_commit)
+
+
+def pack_entries(entries: list, block: int, repo: str, revision: str, source_file: str, model_version: str,
+                 packer_commit: str) -> tuple[bytes, dict]:
+    """Canonical blob from (name, bytes, dtype, shape) entries: name-sorted,
+    64-byte aligned with zero fill (tools/pack_block.py:54-91)."""
+    entries = sorted(entries, key=lambda t: t[0])
     blob = bytearray()
     mentries = []
     for name, data, dtype, shape in entries:
@@ -161,7 +168,7 @@ def pack(bt: BlockTensors, repo: str = "synthetic", revision: str = "synthetic",
         mentries.append({"name": name, "dtype": dtype, "shape": shape, "offset": off, "nbytes": len(data),
                          "sha256": hashlib.sha256(data).hexdigest()})
     manifest = {
-        "packer_version": PACKER_VERSION, "packer_commit": packer_commit, "align": ALIGN, "block": bt.block,
+        "packer_version": PACKER_VERSION, "packer_commit": packer_commit, "align": ALIGN, "block": block,
         "repo": repo, "revision": revision, "source_file": source_file, "model_version": model_version,
         "total_bytes": len(blob), "blob_sha256": hashlib.sha256(bytes(blob)).hexdigest(), "entries": mentries,
     }
@@ -207,3 +214,90 @@ def unpack(blob: bytes, manifest: dict, block: int | None = None) -> BlockTensor
 
 def manifest_json(manifest: dict) -> str:
     return json.dumps(manifest, indent=1)
+
+
+# ---- block directories (the fetch_block.py layout) -------------------------
+
+def quantize_dir(wdir, cls: str = "qkv", gs: int = GROUP, bits: int = 8, scale_dtype: str = "F32") -> list[str]:
+    """Quantise the tensors of class `cls` in a block directory, writing
+    NAME_q8.bin / NAME_q8scale.bin beside the source (tools/quantize_block.py:
+    45-73; the int4 form writes NAME_q4.bin (u4 stored as q + 8) and
+    NAME_q4scale.bin)."""
+    import pathlib
+
+    wdir = pathlib.Path(wdir)
+    man = json.loads((wdir / "manifest.json").read_text())
+    suffixes = [dict((s[0], s[1]) for s in BASE_SPECS)[Q8_BASE[q]] for q in CLASSES[cls]]
+    done = []
+    for name, e in man["tensors"].items():
+        if not any(name.endswith(f"transformer_blocks.{man['block']}.{s}") or name.split(".", 2)[-1] == s
+                   for s in suffixes):
+            continue
+        if e["dtype"] != "BF16":
+            raise ValueError(f"{name}: expected BF16, got {e['dtype']}")
+        raw = np.frombuffer((wdir / e["file"]).read_bytes(), dtype=np.uint16).reshape(e["shape"])
+        q, s = quantize_g128(raw, gs, bits)
+        stem = e["file"].removesuffix(".bin")
+        if bits == 4:
+            (wdir / f"{stem}_q4.bin").write_bytes((q.astype(np.int16) + 8).astype(np.uint8).tobytes())
+            (wdir / f"{stem}_q4scale.bin").write_bytes(s.astype(np.float32).tobytes())
+        else:
+            (wdir / f"{stem}_q8.bin").write_bytes(q.tobytes())
+            sd = s.astype(np.float16) if scale_dtype == "F16" else s.astype(np.float32)
+            (wdir / f"{stem}_q8scale.bin").write_bytes(sd.tobytes())
+        done.append(name)
+    return done
+
+
+def pack_dir(wdir, packer_commit: str = "ltx-mi355x") -> dict:
+    """Pack a block directory into blob.bin + blob_manifest.json
+    (tools/pack_block.py:33-95). A *_q8scale.bin of half the f32 size is
+    recorded as F16."""
+    import pathlib
+
+    wdir = pathlib.Path(wdir)
+    man = json.loads((wdir / "manifest.json").read_text())
+    entries = []
+    for name, e in man["tensors"].items():
+        entries.append((name, (wdir / e["file"]).read_bytes(), e["dtype"], e["shape"]))
+        stem = e["file"].removesuffix(".bin")
+        q8 = wdir / f"{stem}_q8.bin"
+        if q8.exists():
+            o, i = e["shape"]
+            sraw = (wdir / f"{stem}_q8scale.bin").read_bytes()
+            sdt = "F16" if len(sraw) == o * (i // GROUP) * 2 else "F32"
+            entries.append((name + "::q8", q8.read_bytes(), "I8", [o, i]))
+            entries.append((name + "::q8scale", sraw, sdt, [o, i // GROUP]))
+    blob, out = pack_entries(entries, man["block"], man["repo"], man["revision"], man["file"],
+                             man.get("model_version", ""), packer_commit)
+    (wdir / "blob.bin").write_bytes(blob)
+    (wdir / "blob_manifest.json").write_text(manifest_json(out))
+    return out
+
+
+def _main(argv=None) -> int:
+    import argparse
+
+    ap = argparse.ArgumentParser(prog="python -m ltx_amd.blockfmt")
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    q = sub.add_parser("quantize", help="quantise one class of a block directory")
+    q.add_argument("wdir")
+    q.add_argument("--cls", default="qkv", choices=list(CLASSES))
+    q.add_argument("--gs", type=int, default=GROUP)
+    q.add_argument("--bits", type=int, default=8, choices=(4, 8))
+    q.add_argument("--scale-dtype", default="F32", choices=("F32", "F16"))
+    p = sub.add_parser("pack", help="pack a block directory into blob.bin + blob_manifest.json")
+    p.add_argument("wdir")
+    a = ap.parse_args(argv)
+    if a.cmd == "quantize":
+        for n in quantize_dir(a.wdir, a.cls, a.gs, a.bits, a.scale_dtype):
+            print(f"  quantized {n}")
+    else:
+        m = pack_dir(a.wdir)
+        print(f"block {m['block']}: {len(m['entries'])} entries, {m['total_bytes']} bytes, "
+              f"sha256 {m['blob_sha256'][:16]}")
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(_main())

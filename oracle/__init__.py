@@ -208,8 +208,10 @@ def _bf(b):
     return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
-def block_np(bt, inp: dict, cos_thf, sin_thf):
-    """Dense-attention numpy restatement of qBlockOutAll (f64)."""
+def block_np(bt, inp: dict, cos_thf, sin_thf, mistake: str | None = None):
+    """Dense-attention numpy restatement of qBlockOutAll (f64). `mistake`
+    plants one deliberate error (tests use it to show the gates have teeth):
+    layernorm | gate_no_2x | rope_sign | kv_scale | ada_swap."""
     W = {}
     for f in BASE_ORDER[:-2]:
         W[f] = _bf(bt.base[f])
@@ -228,6 +230,8 @@ def block_np(bt, inp: dict, cos_thf, sin_thf):
     cs, sn = cos_thf.astype(np.float64), sin_thf.astype(np.float64)
 
     def rms(a, w=None):
+        if mistake == "layernorm" and w is None:  # mean-subtracting norm instead of RMS
+            a = a - a.mean(-1, keepdims=True)
         r = a / np.sqrt((a * a).mean(-1, keepdims=True) + 1e-6)
         return r * w if w is not None else r
 
@@ -235,7 +239,8 @@ def block_np(bt, inp: dict, cos_thf, sin_thf):
         T = a.shape[0]
         a4 = a.reshape(T, H, 2, 64)
         u, v = a4[:, :, 0], a4[:, :, 1]
-        return np.concatenate([u * cs - v * sn, v * cs + u * sn], -1).reshape(T, D)
+        sg = -1.0 if mistake == "rope_sign" else 1.0
+        return np.concatenate([u * cs - sg * v * sn, v * cs + sg * u * sn], -1).reshape(T, D)
 
     def attn(xq, xkv, p, use_rope):
         q = rms(xq @ W[p + "q_w"].T + W[p + "q_b"], W["qn" + p[-1]])
@@ -244,7 +249,8 @@ def block_np(bt, inp: dict, cos_thf, sin_thf):
         if use_rope:
             q, k = rope(q), rope(k)
         o = sdpa_np(q, k, v)
-        g = 2.0 / (1.0 + np.exp(-(xq @ W["g" + p[-1] + "_w"].T + W["g" + p[-1] + "_b"])))
+        g = (1.0 if mistake == "gate_no_2x" else 2.0) / (1.0 + np.exp(-(xq @ W["g" + p[-1] + "_w"].T
+                                                                         + W["g" + p[-1] + "_b"])))
         o = (o.reshape(-1, H, HD) * g[:, :, None]).reshape(-1, D)
         return o @ W[p + "o_w"].T + W[p + "o_b"]
 
@@ -255,11 +261,13 @@ def block_np(bt, inp: dict, cos_thf, sin_thf):
             W2[f"a{a}{t}_w"] = W[f"{t}{a}_w"]
             W2[f"a{a}{t}_b"] = W[f"{t}{a}_b"]
     W.update(W2)
+    if mistake == "ada_swap":  # shift and scale rows exchanged
+        ada[0], ada[1] = ada[1], ada[0]
     n = rms(x) * (1 + ada[1]) + ada[0]
     x_sa = x + attn(n, n, "a1", True) * ada[2]
     ai = rms(x_sa) * (1 + ada[7]) + ada[6]
     kv = psst + inp["pts2"].astype(np.float64)
-    enc = ctx * (1 + kv[1]) + kv[0]
+    enc = ctx * (kv[1] if mistake == "kv_scale" else 1 + kv[1]) + kv[0]
     x_ca = x_sa + attn(ai, enc, "a2", False) * ada[8]
     fi = rms(x_ca) * (1 + ada[4]) + ada[3]
     h = fi @ W["ff1_w"].T
