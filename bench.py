@@ -28,6 +28,10 @@ sys.path.insert(0, str(ROOT))
 
 D, H, HD, FF = 4096, 32, 128, 16384
 PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
+# HBM bytes per self-attention launch from rocprofv3 FETCH_SIZE (x2.0, the
+# factor a 1 GiB copy calibrates) + WRITE_SIZE (x1.0), for the kernel as
+# built at that measurement (profiles/attn_self_t28672_f16_hbm_bytes.md).
+ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.478e9}
 
 
 def flops(T: int, S: int) -> dict:
@@ -96,6 +100,9 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=28672)
     ap.add_argument("--text", type=int, default=256)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="run one plain device-to-device copy of this many MiB before the timed steps "
+                         "(the known-size kernel that calibrates HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "single-GPU build: the block runs on one MI355X; multi-GPU sharding is a "
@@ -126,6 +133,13 @@ def main() -> int:
     def step():
         ctx.forward(w, x, tstab, tidx, c, pts2, dcos, dsin, y, mode=mode, stream=stream)
 
+    if args.copy_calib_mib:
+        src = torch.empty(args.copy_calib_mib << 18, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"bench: calibration copy of {args.copy_calib_mib} MiB done")
+        del src, dst
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -172,7 +186,8 @@ def main() -> int:
         "gemm_tflops": round(f["gemm"] / (gemm_ms * 1e-3) / 1e12, 1) if gemm_ms else None,
         "kernel_ms": per,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_TFLOPS, 4),
+                     "traffic": ATTN_SELF_TRAFFIC.get((T, args.mode)),
                      "kernel": "ltx_attn_" + args.mode + " (self-attention, 4*H*T^2*HD = "
                                f"{f['self_attn'] / 1e12:.3f} TFLOP per launch)"},
     }
