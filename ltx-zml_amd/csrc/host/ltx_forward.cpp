@@ -136,9 +136,10 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
     g.tiles_m = (M + 255) / 256;
     g.tiles_n = p.N / 256;
     char name[64];
-    std::snprintf(name, sizeof(name), "ltx_gemm_%s_%s_%s", msuffix(mode), bk,
-                  epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv");
-    c->launch(name, g.tiles_m * g.tiles_n, 1, 1, 256, &g, st, label);
+    std::snprintf(name, sizeof(name), "ltx_gemm_%s_%s_%s%s", msuffix(mode), bk,
+                  epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv",
+                  c->gemm_waves == 8 ? "_w8" : "");
+    c->launch(name, g.tiles_m * g.tiles_n, 1, 1, 64 * c->gemm_waves, &g, st, label);
 }
 
 static void gate16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M, float* out, hipStream_t st) {
@@ -164,7 +165,9 @@ static void attn16(ltx_ctx* c, int mode, const void* q, const void* k, const voi
     a.lkv = lkv;
     a.scale_log2 = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;
     a.q_tiles = (lq + 255) / 256;
-    c->launch(mode == LTX_MODE_BF16 ? "ltx_attn_bf16" : "ltx_attn_f16", a.q_tiles * LTX_H, 1, 1, 256, &a, st, label);
+    const bool w8 = c->attn_waves == 8;
+    c->launch(mode == LTX_MODE_BF16 ? (w8 ? "ltx_attn_bf16_w8" : "ltx_attn_bf16") : (w8 ? "ltx_attn_f16_w8" : "ltx_attn_f16"),
+              a.q_tiles * LTX_H, 1, 1, w8 ? 512 : 256, &a, st, label);
 }
 
 // f32-mode GEMM over rows [r0, r0 + N) of a (possibly fused) projection.

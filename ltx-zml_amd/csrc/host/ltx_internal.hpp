@@ -70,6 +70,9 @@ struct ltx_block_weights {
 
 struct ltx_ctx {
     int device = 0;
+    // kernel variants: waves per workgroup of the GEMM (4 or 8) and attention (4 or 8)
+    int gemm_waves = 8;
+    int attn_waves = 8;
     std::vector<hipModule_t> modules;
     std::map<std::string, hipFunction_t> fns;
     std::string err;

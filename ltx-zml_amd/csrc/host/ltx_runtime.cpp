@@ -141,6 +141,9 @@ int ltx_init(int device, ltx_ctx** out) {
             throw ltx::Error(std::string("ltx_init: code objects are gfx950-only, device is ") + prop.gcnArchName);
         c = new ltx_ctx();
         c->device = device;
+        // variant overrides (used for A/B timing): 4 or 8 waves per workgroup
+        if (const char* e = std::getenv("LTX_GEMM_WAVES")) c->gemm_waves = std::atoi(e) == 4 ? 4 : 8;
+        if (const char* e = std::getenv("LTX_ATTN_WAVES")) c->attn_waves = std::atoi(e) == 4 ? 4 : 8;
         for (const unsigned char* co : {ltx_co_k_gemm, ltx_co_k_attn, ltx_co_k_norm, ltx_co_k_f32}) {
             hipModule_t m;
             HIPC(hipModuleLoadData(&m, co));

@@ -20,15 +20,19 @@
 // as in the reference, and keys past lkv are masked to -inf.
 #include "ltx_device.h"
 
-#define QW 64          // queries per wave
 #define QT 256         // queries per workgroup
 #define KT 64          // keys per tile
 #define KROW (128 + 8) // padded K row (16-bit elements)
 #define VROW (KT + 8)  // padded V^T row
 
-template <typename T>
+// QB = 32-query column blocks per wave: 2 -> 4 waves of 64 queries (one wave
+// per SIMD), 1 -> 8 waves of 32 queries (two waves per SIMD, so one wave's
+// softmax VALU work overlaps the other's MFMAs).
+template <typename T, int QB>
 __device__ void attn_body(const LtxAttnArgs& a) {
     typedef typename Op<T>::v8 v8;
+    constexpr int NT = 256 * (2 / QB);  // threads per workgroup
+    constexpr int QW = 32 * QB;         // queries per wave
     __shared__ __attribute__((aligned(16))) uint16_t sK[2][KT * KROW];
     __shared__ __attribute__((aligned(16))) uint16_t sV[2][LTX_HD * VROW];
 
@@ -46,35 +50,41 @@ __device__ void attn_body(const LtxAttnArgs& a) {
 
     // Q^T operand: lane holds Q[q][16 c + 8 (lane / 32) .. + 8] for its query.
     const int fr = lane & 31, hi = lane >> 5;
-    v8 qf[2][8];
+    v8 qf[QB][8];
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
+    for (int qb = 0; qb < QB; qb++) {
         const int q = min(q0 + 32 * qb + fr, lq - 1);
 #pragma unroll
         for (int c = 0; c < 8; c++) qf[qb][c] = __builtin_bit_cast(v8, *(const u32x4*)(Q + (size_t)q * LTX_HD + 16 * c + 8 * hi));
     }
 
-    f32x16 o[2][4];
+    f32x16 o[QB][4];
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++)
+    for (int qb = 0; qb < QB; qb++)
 #pragma unroll
         for (int db = 0; db < 4; db++) o[qb][db] = f32x16{0};
-    float m[2] = {-3.402823466e38f, -3.402823466e38f}, l[2] = {0.f, 0.f};
+    float m[QB], l[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; qb++) {
+        m[qb] = -3.402823466e38f;
+        l[qb] = 0.f;
+    }
     const float C = a.scale_log2;
 
     // Global -> register staging of one K tile (64 x 128) and one V^T tile
-    // (128 x 64): 4 + 4 chunks of 16 B per thread.
-    u32x4 rk[4], rv[4];
+    // (128 x 64): 1024 + 1024 chunks of 16 B per workgroup.
+    constexpr int NCH = 1024 / NT;
+    u32x4 rk[NCH], rv[NCH];
     auto gload = [&](int kv0) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            int id = tid + 256 * i, row = id >> 4, c16 = id & 15;
+        for (int i = 0; i < NCH; i++) {
+            int id = tid + NT * i, row = id >> 4, c16 = id & 15;
             int key = min(kv0 + row, lkv - 1);
             rk[i] = *(const u32x4*)(K + (size_t)key * LTX_HD + 8 * c16);
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            int id = tid + 256 * i, d = id >> 3, kc = id & 7;
+        for (int i = 0; i < NCH; i++) {
+            int id = tid + NT * i, d = id >> 3, kc = id & 7;
             int key = kv0 + 8 * kc;
             const uint16_t* src = V + (size_t)d * lkv + key;
             if (key + 8 <= lkv && (lkv & 7) == 0) {  // 16-byte aligned row chunk
@@ -90,13 +100,13 @@ __device__ void attn_body(const LtxAttnArgs& a) {
     };
     auto sstore = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            int id = tid + 256 * i, row = id >> 4, c16 = id & 15;
+        for (int i = 0; i < NCH; i++) {
+            int id = tid + NT * i, row = id >> 4, c16 = id & 15;
             *(u32x4*)(sK[buf] + row * KROW + 8 * c16) = rk[i];
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            int id = tid + 256 * i, d = id >> 3, kc = id & 7;
+        for (int i = 0; i < NCH; i++) {
+            int id = tid + NT * i, d = id >> 3, kc = id & 7;
             int base = 16 * (kc >> 1), odd = kc & 1;
             uint16_t* row = sV[buf] + d * VROW + base;
             *(u32x2*)(row + (odd ? 4 : 0)) = u32x2{rv[i][0], rv[i][1]};   // keys 0-3 / 8-11
@@ -114,11 +124,11 @@ __device__ void attn_body(const LtxAttnArgs& a) {
         if (tix + 1 < ntiles) gload(kv0 + KT);
 
         // S^T blocks: s[kb][qb] = K[32 kb .. +32] . Q^T[qb]
-        f32x16 s[2][2];
+        f32x16 s[2][QB];
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-            for (int qb = 0; qb < 2; qb++) s[kb][qb] = f32x16{0};
+            for (int qb = 0; qb < QB; qb++) s[kb][qb] = f32x16{0};
         const uint16_t* pk = sK[buf] + fr * KROW + 8 * hi;
 #pragma unroll
         for (int c = 0; c < 8; c++) {
@@ -126,14 +136,14 @@ __device__ void attn_body(const LtxAttnArgs& a) {
             for (int kb = 0; kb < 2; kb++) {
                 v8 kf = __builtin_bit_cast(v8, *(const u32x4*)(pk + 32 * kb * KROW + 16 * c));
 #pragma unroll
-                for (int qb = 0; qb < 2; qb++) s[kb][qb] = Op<T>::mfma32(kf, qf[qb][c], s[kb][qb]);
+                for (int qb = 0; qb < QB; qb++) s[kb][qb] = Op<T>::mfma32(kf, qf[qb][c], s[kb][qb]);
             }
         }
 
         // Online softmax per query column (lane-local), P^T operands.
-        v8 pf[2][4];
+        v8 pf[QB][4];
 #pragma unroll
-        for (int qb = 0; qb < 2; qb++) {
+        for (int qb = 0; qb < QB; qb++) {
             if (kv0 + KT > lkv) {
 #pragma unroll
                 for (int kb = 0; kb < 2; kb++)
@@ -181,7 +191,7 @@ __device__ void attn_body(const LtxAttnArgs& a) {
             for (int db = 0; db < 4; db++) {
                 v8 vf = __builtin_bit_cast(v8, *(const u32x4*)(pv + 32 * db * VROW + 16 * kc));
 #pragma unroll
-                for (int qb = 0; qb < 2; qb++) o[qb][db] = Op<T>::mfma32(vf, pf[qb][kc], o[qb][db]);
+                for (int qb = 0; qb < QB; qb++) o[qb][db] = Op<T>::mfma32(vf, pf[qb][kc], o[qb][db]);
             }
         }
 
@@ -192,7 +202,7 @@ __device__ void attn_body(const LtxAttnArgs& a) {
     // out[q][h * 128 + d] = O^T[d][q] / l * 2 sigmoid(glog[q][h])
     uint16_t* out = (uint16_t*)a.out;
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
+    for (int qb = 0; qb < QB; qb++) {
         const float lt = l[qb] + __shfl_xor(l[qb], 32, 64);
         const int q = q0 + 32 * qb + fr;
         if (q >= lq) continue;
@@ -211,5 +221,7 @@ __device__ void attn_body(const LtxAttnArgs& a) {
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256, 1) ltx_attn_f16(const LtxAttnArgs a) { attn_body<_Float16>(a); }
-extern "C" __global__ void __launch_bounds__(256, 1) ltx_attn_bf16(const LtxAttnArgs a) { attn_body<__bf16>(a); }
+extern "C" __global__ void __launch_bounds__(256, 1) ltx_attn_f16(const LtxAttnArgs a) { attn_body<_Float16, 2>(a); }
+extern "C" __global__ void __launch_bounds__(256, 1) ltx_attn_bf16(const LtxAttnArgs a) { attn_body<__bf16, 2>(a); }
+extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_f16_w8(const LtxAttnArgs a) { attn_body<_Float16, 1>(a); }
+extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_bf16_w8(const LtxAttnArgs a) { attn_body<__bf16, 1>(a); }

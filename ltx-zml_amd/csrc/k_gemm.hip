@@ -1,15 +1,16 @@
 // W8A16 / W16A16 GEMM for gfx950: y[M][N] = A[M][K] . W[N][K]^T with fused
 // epilogues (bias, GELU-tanh, gated residual, QKV split with V^T store).
 //
-// Tile 256 x 256 x 64, 256 threads = 4 waves in a 2 x 2 grid, each wave owning
-// a 128 x 128 sub-tile = 4 x 4 MFMA blocks of v_mfma_f32_32x32x16_{f16,bf16}
-// (fp32 accumulate). Global -> register -> LDS staging with two LDS buffers
-// and one barrier per K-tile. int8 weights are dequantised ONCE per workgroup
+// Tile 256 x 256 x 64 per workgroup of NW waves: NW = 4 (a 2 x 2 grid of
+// 128 x 128 wave tiles, one wave per SIMD) or NW = 8 (2 x 4 grid of 128 x 64
+// wave tiles, two waves per SIMD so one wave's dequant/LDS work overlaps the
+// other's MFMAs). v_mfma_f32_32x32x16_{f16,bf16}, fp32 accumulate.
+// Global -> register -> LDS staging with two LDS buffers and one barrier per
+// K-tile; MFMA fragments double-buffered in registers. int8 weights are dequantised ONCE per workgroup
 // while staging into LDS: v = fma(u, s, -128 s) with u = q + 128 (an unsigned
 // byte), which is the single-rounding f32 value q * s of dq4
 // (ltx/block.zig:462-471), then rounded to the 16-bit operand type.
-// LDS rows are padded by 16 bytes so the 32 rows a fragment read touches hit
-// distinct banks.
+// LDS rows are padded by 16 bytes.
 #include "ltx_device.h"
 
 #define BM 256
@@ -40,35 +41,38 @@ __device__ __forceinline__ TileIdx tile_of(int bid, int tiles_m, int tiles_n) {
     return ti;
 }
 
-template <typename T, int BKIND>
+template <typename T, int BKIND, int NT>
 struct Stage {
-    // A: 8 x 16 B per thread; B: int8 4 x 16 B, or 16-bit 8 x 16 B.
-    u32x4 ra[8];
-    u32x4 rb[8];
-    float sc[4];
+    static constexpr int NA = BM * (BK / 8) / NT;    // 16-byte A chunks per thread
+    static constexpr int NB8 = BN * (BK / 16) / NT;  // 16-byte int8 B chunks per thread
+    static constexpr int NB16 = BN * (BK / 8) / NT;  // 16-byte 16-bit B chunks per thread
+    static constexpr int NBR = BKIND == LTX_B_W16 ? NB16 : NB8;
+    u32x4 ra[NA];
+    u32x4 rb[NBR];
+    float sc[NB8];
 
     __device__ __forceinline__ void load(const LtxGemmArgs& a, int m0, int n0, int k0, int tid) {
         const uint16_t* A = (const uint16_t*)a.a;
-        int c = tid & 7;
+        const int c = tid & 7;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            int r = min(m0 + (tid >> 3) + 32 * i, a.M - 1);
+        for (int i = 0; i < NA; i++) {
+            int r = min(m0 + (tid >> 3) + (NT / 8) * i, a.M - 1);
             ra[i] = *(const u32x4*)(A + (size_t)r * a.lda + k0 + 8 * c);
         }
         if (BKIND == LTX_B_W16) {
             const uint16_t* B = (const uint16_t*)a.b;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                int r = n0 + (tid >> 3) + 32 * i;
+            for (int i = 0; i < NB16; i++) {
+                int r = n0 + (tid >> 3) + (NT / 8) * i;
                 rb[i] = *(const u32x4*)(B + (size_t)r * a.K + k0 + 8 * c);
             }
         } else {
             const int8_t* B = (const int8_t*)a.b;
-            int cb = tid & 3;
-            int G = a.K / LTX_GROUP;
+            const int cb = tid & 3;
+            const int G = a.K / LTX_GROUP;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                int r = n0 + (tid >> 2) + 64 * i;
+            for (int i = 0; i < NB8; i++) {
+                int r = n0 + (tid >> 2) + (NT / 4) * i;
                 rb[i] = *(const u32x4*)(B + (size_t)r * a.K + k0 + 16 * cb);
                 size_t si = (size_t)r * G + (k0 + 16 * cb) / LTX_GROUP;
                 sc[i] = BKIND == LTX_B_I8_F16S ? f16_bits_to_f32(((const uint16_t*)a.scales)[si])
@@ -78,17 +82,17 @@ struct Stage {
     }
 
     __device__ __forceinline__ void store(uint16_t* sA, uint16_t* sB, int tid) {
-        int c = tid & 7;
+        const int c = tid & 7;
 #pragma unroll
-        for (int i = 0; i < 8; i++) *(u32x4*)(sA + ((tid >> 3) + 32 * i) * LDSW + 8 * c) = ra[i];
+        for (int i = 0; i < NA; i++) *(u32x4*)(sA + ((tid >> 3) + (NT / 8) * i) * LDSW + 8 * c) = ra[i];
         if (BKIND == LTX_B_W16) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) *(u32x4*)(sB + ((tid >> 3) + 32 * i) * LDSW + 8 * c) = rb[i];
+            for (int i = 0; i < NB16; i++) *(u32x4*)(sB + ((tid >> 3) + (NT / 8) * i) * LDSW + 8 * c) = rb[i];
         } else {
-            int cb = tid & 3;
+            const int cb = tid & 3;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float s = sc[i], nb = -128.0f * s;
+            for (int i = 0; i < NB8; i++) {
+                const float s = sc[i], nb = -128.0f * s;
                 uint32_t o[8];
 #pragma unroll
                 for (int d = 0; d < 4; d++) {
@@ -96,7 +100,7 @@ struct Stage {
                     o[2 * d] = deq_pack2<T>((float)(w & 0xffu), (float)((w >> 8) & 0xffu), s, nb);
                     o[2 * d + 1] = deq_pack2<T>((float)((w >> 16) & 0xffu), (float)(w >> 24), s, nb);
                 }
-                uint16_t* dst = sB + ((tid >> 2) + 64 * i) * LDSW + 16 * cb;
+                uint16_t* dst = sB + ((tid >> 2) + (NT / 4) * i) * LDSW + 16 * cb;
                 *(u32x4*)dst = u32x4{o[0], o[1], o[2], o[3]};
                 *(u32x4*)(dst + 8) = u32x4{o[4], o[5], o[6], o[7]};
             }
@@ -104,66 +108,87 @@ struct Stage {
     }
 };
 
-template <typename T, int BKIND, int EPI>
+template <typename T, int BKIND, int EPI, int NW>
 __device__ void gemm_body(const LtxGemmArgs& a) {
     typedef typename Op<T>::v8 v8;
+    constexpr int NT = 64 * NW;
+    constexpr int WNW = NW / 2;          // waves along N
+    constexpr int WN = BN / WNW;         // wave tile N extent (128 or 64)
+    constexpr int NI = 4, NJ = WN / 32;  // 32 x 32 MFMA blocks per wave
     __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * LDSW];
     __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN * LDSW];
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int wm = w >> 1, wn = w & 1;
+    const int wm = w / WNW, wn = w % WNW;
     TileIdx ti = tile_of(blockIdx.x, a.tiles_m, a.tiles_n);
     const int m0 = ti.tm * BM, n0 = ti.tn * BN;
 
-    f32x16 acc[4][4];
+    f32x16 acc[NI][NJ];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < NI; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f32x16{0};
+        for (int j = 0; j < NJ; j++) acc[i][j] = f32x16{0};
 
-    Stage<T, BKIND> st;
+    Stage<T, BKIND, NT> st;
     const int nk = a.K / BK;
     st.load(a, m0, n0, 0, tid);
     st.store(sA[0], sB[0], tid);
     __syncthreads();
 
+    // Fragments are double-buffered in registers: the LDS reads for k-step
+    // kk + 1 are issued before the MFMAs of step kk; the next K-tile's global
+    // loads are issued at the top of the tile and written to the other LDS
+    // buffer after the MFMAs.
     const int fr = lane & 31, fk = 8 * (lane >> 5);
+    const int offa = (wm * 128 + fr) * LDSW + fk, offb = (wn * WN + fr) * LDSW + fk;
+    v8 fa[2][NI], fb[2][NJ];
+    auto frags = [&](int buf, int kk, int slot) {
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            fa[slot][i] = __builtin_bit_cast(v8, *(const u32x4*)(sA[buf] + offa + 32 * i * LDSW + 16 * kk));
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            fb[slot][j] = __builtin_bit_cast(v8, *(const u32x4*)(sB[buf] + offb + 32 * j * LDSW + 16 * kk));
+    };
+    frags(0, 0, 0);
     for (int kt = 0; kt < nk; kt++) {
         const int buf = kt & 1;
-        if (kt + 1 < nk) st.load(a, m0, n0, (kt + 1) * BK, tid);
-        const uint16_t* pa = sA[buf] + (wm * 128 + fr) * LDSW + fk;
-        const uint16_t* pb = sB[buf] + (wn * 128 + fr) * LDSW + fk;
+        const bool more = kt + 1 < nk;
+        if (more) st.load(a, m0, n0, (kt + 1) * BK, tid);
 #pragma unroll
         for (int kk = 0; kk < BK / 16; kk++) {
-            v8 fa[4], fb[4];
+            const int cur = kk & 1;
+            if (kk + 1 < BK / 16) frags(buf, kk + 1, cur ^ 1);
 #pragma unroll
-            for (int i = 0; i < 4; i++) fa[i] = __builtin_bit_cast(v8, *(const u32x4*)(pa + 32 * i * LDSW + 16 * kk));
+            for (int i = 0; i < NI; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) fb[j] = __builtin_bit_cast(v8, *(const u32x4*)(pb + 32 * j * LDSW + 16 * kk));
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = Op<T>::mfma32(fa[i], fb[j], acc[i][j]);
+                for (int j = 0; j < NJ; j++) acc[i][j] = Op<T>::mfma32(fa[cur][i], fb[cur][j], acc[i][j]);
         }
-        if (kt + 1 < nk) st.store(sA[buf ^ 1], sB[buf ^ 1], tid);
+        if (more) st.store(sA[buf ^ 1], sB[buf ^ 1], tid);
         __syncthreads();
+        if (more) frags(buf ^ 1, 0, 0);
     }
 
     // Epilogue. acc[i][j][r] sits at row 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4
-    // and column 32 j + lane % 32 of this wave's 128 x 128 sub-tile.
+    // and column 32 j + lane % 32 of this wave's sub-tile.
     const int rb = m0 + wm * 128 + 4 * (lane >> 5);
-    const int cb = n0 + wn * 128 + (lane & 31);
+    const int cb = n0 + wn * WN + (lane & 31);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int n = cb + 32 * j;
-        const float bias = a.bias ? a.bias[n] : 0.0f;
+    for (int i = 0; i < NI; i++) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int r = 0; r < 16; r++) {
+            const int m = rb + 32 * i + 8 * (r >> 2) + (r & 3);
+            if (m >= a.M) continue;
+            const float* gt = nullptr;
+            const float* gs = nullptr;
+            if (EPI == LTX_EPI_RESID_GATE) {  // ada row of the gate: sst[i] + tstab[tidx[m]][i]
+                gt = a.ada.tstab + ((size_t)a.ada.tidx[m] * 9 + a.igate) * LTX_D;
+                gs = a.ada.sst + (size_t)a.igate * LTX_D;
+            }
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = rb + 32 * i + 8 * (r >> 2) + (r & 3);
-                if (m >= a.M) continue;
-                float v = acc[i][j][r] + bias;
+            for (int j = 0; j < NJ; j++) {
+                const int n = cb + 32 * j;
+                float v = acc[i][j][r] + (a.bias ? a.bias[n] : 0.0f);
                 if (EPI == LTX_EPI_STORE) {
                     if (a.gelu) v = gelu_tanh(v);
                     if (a.out_f32)
@@ -172,7 +197,7 @@ __device__ void gemm_body(const LtxGemmArgs& a) {
                         ((uint16_t*)a.out)[(size_t)m * a.ldo + n] = Op<T>::bits(v);
                 } else if (EPI == LTX_EPI_RESID_GATE) {
                     size_t o = (size_t)m * a.ldo + n;
-                    ((float*)a.out)[o] = a.resid[o] + v * ada_val(a.ada, m, a.igate, n);
+                    ((float*)a.out)[o] = a.resid[o] + v * (gt[n] + gs[n]);
                 } else {  // QKV
                     if (n0 < a.nsplit) {
                         ((float*)a.out)[(size_t)m * a.nsplit + n] = v;
@@ -188,7 +213,10 @@ __device__ void gemm_body(const LtxGemmArgs& a) {
 
 #define GEMM_KERNEL(NAME, T, BK_, EPI_)                                                        \
     extern "C" __global__ void __launch_bounds__(256, 1) NAME(const LtxGemmArgs a) {           \
-        gemm_body<T, BK_, EPI_>(a);                                                            \
+        gemm_body<T, BK_, EPI_, 4>(a);                                                         \
+    }                                                                                          \
+    extern "C" __global__ void __launch_bounds__(512, 1) NAME##_w8(const LtxGemmArgs a) {      \
+        gemm_body<T, BK_, EPI_, 8>(a);                                                         \
     }
 
 GEMM_KERNEL(ltx_gemm_f16_i8f32_store, _Float16, LTX_B_I8_F32S, LTX_EPI_STORE)
