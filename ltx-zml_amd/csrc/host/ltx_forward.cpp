@@ -164,10 +164,13 @@ static void attn16(ltx_ctx* c, int mode, const void* q, const void* k, const voi
     a.lq = lq;
     a.lkv = lkv;
     a.scale_log2 = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;
-    a.q_tiles = (lq + 255) / 256;
-    const bool w8 = c->attn_waves == 8;
-    c->launch(mode == LTX_MODE_BF16 ? (w8 ? "ltx_attn_bf16_w8" : "ltx_attn_bf16") : (w8 ? "ltx_attn_f16_w8" : "ltx_attn_f16"),
-              a.q_tiles * LTX_H, 1, 1, w8 ? 512 : 256, &a, st, label);
+    const int v = c->attn_variant;
+    a.q_tiles = (lq + 255) / 256;                    // 256 queries per workgroup
+    const bool full = v != 0 && lkv % 64 == 0;       // key length a whole number of 64-key tiles
+    char name[48];
+    std::snprintf(name, sizeof(name), "ltx_attn_%s%s%s", msuffix(mode), v == 0 ? "" : v == 1 ? "_w8" : "_ps",
+                  full ? "_full" : "");
+    c->launch(name, a.q_tiles * LTX_H, 1, 1, v == 0 ? 256 : 512, &a, st, label);
 }
 
 // f32-mode GEMM over rows [r0, r0 + N) of a (possibly fused) projection.

@@ -72,7 +72,7 @@ struct ltx_ctx {
     int device = 0;
     // kernel variants: waves per workgroup of the GEMM (4 or 8) and attention (4 or 8)
     int gemm_waves = 8;
-    int attn_waves = 8;
+    int attn_variant = 1;  // 0: 4 waves x 64 queries, 1: 8 waves x 32, 2: 8 waves, halves phase-shifted
     std::vector<hipModule_t> modules;
     std::map<std::string, hipFunction_t> fns;
     std::string err;

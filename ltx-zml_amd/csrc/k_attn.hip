@@ -2,39 +2,48 @@
 // ltx/block.zig:105-154, whileSdpaC), fused with the per-(token, head) gate
 // 2*sigmoid(glog) and the head merge (ltx/block.zig:237-242).
 //
-// Workgroup = 4 waves = 256 queries of one head; each wave owns 64 queries
-// (two 32-query column blocks). K and V^T are streamed through LDS in tiles
-// of 64 keys, double-buffered (global -> registers -> LDS, one barrier per
-// tile). Scores are computed TRANSPOSED, S^T = K . Q^T, and the output as
-// O^T = V^T . P^T, with v_mfma_f32_32x32x16: the query is then the MFMA column
-// index, so lane l always holds query l % 32 — its running max m, partial sum
-// l and its O^T column stay lane-local, and only the tile max needs one
-// exchange with lane l ^ 32. The P^T operand comes straight from the S^T
-// accumulators (no LDS round trip): within every 16-key chunk the keys are
-// consumed in the order 0-3, 8-11, 4-7, 12-15, which is exactly the order the
-// accumulator layout hands them to each lane, and the V^T tile is stored in
-// LDS permuted the same way.
+// A workgroup owns QT queries of one head; each wave owns QW = 32 * QB of
+// them. K and V^T are streamed through LDS in tiles of 64 keys (global ->
+// registers -> LDS, one barrier per tile). Scores are computed TRANSPOSED,
+// S^T = K . Q^T, and the output as O^T = V^T . P^T, with v_mfma_f32_32x32x16:
+// the query is then the MFMA column index, so lane l always holds query
+// l % 32 — its running max m, partial sum l and its O^T column stay
+// lane-local, and only the tile max needs one exchange with lane l ^ 32.
+// The P^T operand comes straight from the S^T accumulators (no LDS round
+// trip): within every 16-key chunk the keys are consumed in the order 0-3,
+// 8-11, 4-7, 12-15, which is the order the accumulator layout hands them to
+// each lane, and the V^T tile is stored in LDS permuted the same way.
+//
+// Eight-wave variant (two waves per SIMD) runs the two halves of the
+// workgroup half a tile apart: waves 0-3 do S(j), softmax(j), PV(j) while
+// waves 4-7 do softmax(j-1), PV(j-1), S(j). Within one barrier interval one
+// half issues MFMAs while the other half runs the softmax VALU work, instead
+// of both contending for the same unit at the same time. This needs the V
+// tile of j-1 alive during iteration j: K/V use three LDS buffers.
 //
 // Statistics are f32. Softmax uses exp2 with the 1/sqrt(128) scale folded
 // into the exponent (s * C - m * C, C = scale * log2 e); m starts at -FLT_MAX
-// as in the reference, and keys past lkv are masked to -inf.
+// as in the reference, and keys past lkv are masked to -inf. The running max
+// moves only when a query's tile max exceeds it by more than 2^8 in p; the
+// stale max is otherwise kept for numerator and denominator alike.
 #include "ltx_device.h"
 
-#define QT 256         // queries per workgroup
-#define KT 64          // keys per tile
-#define KROW (128 + 8) // padded K row (16-bit elements)
-#define VROW (KT + 8)  // padded V^T row
+#define KT 64              // keys per tile
+#define KROW (128 + 8)     // padded K row (16-bit elements)
+#define VROW (KT + 8)      // padded V^T row
+#define RESCALE_LOG2 8.0f  // rescale threshold, in log2 units of p
 
-// QB = 32-query column blocks per wave: 2 -> 4 waves of 64 queries (one wave
-// per SIMD), 1 -> 8 waves of 32 queries (two waves per SIMD, so one wave's
-// softmax VALU work overlaps the other's MFMAs).
-template <typename T, int QB>
+// QB: 32-query column blocks per wave. NW: waves per workgroup. FULL: lkv is
+// a multiple of 64 (no tail handling, no masking). PS: phase-shifted halves.
+template <typename T, int QB, bool FULL, int NW, bool PS>
 __device__ void attn_body(const LtxAttnArgs& a) {
     typedef typename Op<T>::v8 v8;
-    constexpr int NT = 256 * (2 / QB);  // threads per workgroup
+    constexpr int NT = 64 * NW;         // threads per workgroup
+    constexpr int QT = NW * 32 * QB;    // queries per workgroup
     constexpr int QW = 32 * QB;         // queries per wave
-    __shared__ __attribute__((aligned(16))) uint16_t sK[2][KT * KROW];
-    __shared__ __attribute__((aligned(16))) uint16_t sV[2][LTX_HD * VROW];
+    constexpr int NBUF = PS ? 3 : 2;    // LDS tile buffers
+    __shared__ __attribute__((aligned(16))) uint16_t sK[NBUF][KT * KROW];
+    __shared__ __attribute__((aligned(16))) uint16_t sV[NBUF][LTX_HD * VROW];
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int nblk = a.q_tiles * LTX_H;
@@ -55,17 +64,16 @@ __device__ void attn_body(const LtxAttnArgs& a) {
     for (int qb = 0; qb < QB; qb++) {
         const int q = min(q0 + 32 * qb + fr, lq - 1);
 #pragma unroll
-        for (int c = 0; c < 8; c++) qf[qb][c] = __builtin_bit_cast(v8, *(const u32x4*)(Q + (size_t)q * LTX_HD + 16 * c + 8 * hi));
+        for (int c = 0; c < 8; c++)
+            qf[qb][c] = __builtin_bit_cast(v8, *(const u32x4*)(Q + (size_t)q * LTX_HD + 16 * c + 8 * hi));
     }
 
     f32x16 o[QB][4];
-#pragma unroll
-    for (int qb = 0; qb < QB; qb++)
-#pragma unroll
-        for (int db = 0; db < 4; db++) o[qb][db] = f32x16{0};
     float m[QB], l[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; qb++) {
+#pragma unroll
+        for (int db = 0; db < 4; db++) o[qb][db] = f32x16{0};
         m[qb] = -3.402823466e38f;
         l[qb] = 0.f;
     }
@@ -79,7 +87,7 @@ __device__ void attn_body(const LtxAttnArgs& a) {
 #pragma unroll
         for (int i = 0; i < NCH; i++) {
             int id = tid + NT * i, row = id >> 4, c16 = id & 15;
-            int key = min(kv0 + row, lkv - 1);
+            int key = FULL ? kv0 + row : min(kv0 + row, lkv - 1);
             rk[i] = *(const u32x4*)(K + (size_t)key * LTX_HD + 8 * c16);
         }
 #pragma unroll
@@ -87,7 +95,7 @@ __device__ void attn_body(const LtxAttnArgs& a) {
             int id = tid + NT * i, d = id >> 3, kc = id & 7;
             int key = kv0 + 8 * kc;
             const uint16_t* src = V + (size_t)d * lkv + key;
-            if (key + 8 <= lkv && (lkv & 7) == 0) {  // 16-byte aligned row chunk
+            if (FULL || (key + 8 <= lkv && (lkv & 7) == 0)) {  // 16-byte aligned row chunk
                 rv[i] = *(const u32x4*)src;
             } else {  // ragged tail / unaligned rows: element loads, zero-fill (0 * p stays finite)
                 uint16_t e[8];
@@ -114,17 +122,9 @@ __device__ void attn_body(const LtxAttnArgs& a) {
         }
     };
 
-    const int ntiles = (lkv + KT - 1) / KT;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-
-    for (int tix = 0; tix < ntiles; tix++) {
-        const int buf = tix & 1, kv0 = tix * KT;
-        if (tix + 1 < ntiles) gload(kv0 + KT);
-
-        // S^T blocks: s[kb][qb] = K[32 kb .. +32] . Q^T[qb]
-        f32x16 s[2][QB];
+    // S^T blocks of one tile: s[kb][qb] = K[32 kb .. +32] . Q^T[qb]
+    typedef f32x16 STile[2][QB];
+    auto scores = [&](const int buf, STile& s) {
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
@@ -139,12 +139,14 @@ __device__ void attn_body(const LtxAttnArgs& a) {
                 for (int qb = 0; qb < QB; qb++) s[kb][qb] = Op<T>::mfma32(kf, qf[qb][c], s[kb][qb]);
             }
         }
+    };
 
-        // Online softmax per query column (lane-local), P^T operands.
-        v8 pf[QB][4];
+    // Online softmax of one tile (lane-local per query) -> P^T operands.
+    typedef v8 PTile[QB][4];
+    auto softmax = [&](STile& s, PTile& pf, const int kv0, const bool last) {
 #pragma unroll
         for (int qb = 0; qb < QB; qb++) {
-            if (kv0 + KT > lkv) {
+            if (!FULL && last && kv0 + KT > lkv) {
 #pragma unroll
                 for (int kb = 0; kb < 2; kb++)
 #pragma unroll
@@ -159,10 +161,15 @@ __device__ void attn_body(const LtxAttnArgs& a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[1][qb][r]);
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mn = fmaxf(m[qb], mx);
-            const float corr = __builtin_amdgcn_exp2f((m[qb] - mn) * C);
-            const float mc = mn * C;
-            m[qb] = mn;
+            if (__builtin_amdgcn_ballot_w64(mx > m[qb] + RESCALE_LOG2 / C) != 0) {
+                const float mn = fmaxf(m[qb], mx);
+                const float corr = __builtin_amdgcn_exp2f((m[qb] - mn) * C);
+                m[qb] = mn;
+                l[qb] *= corr;
+#pragma unroll
+                for (int db = 0; db < 4; db++) o[qb][db] *= corr;
+            }
+            const float mc = m[qb] * C;
             float ps = 0.f;
 #pragma unroll
             for (int kb = 0; kb < 2; kb++) {
@@ -170,33 +177,76 @@ __device__ void attn_body(const LtxAttnArgs& a) {
                 for (int half = 0; half < 2; half++) {
                     float p[8];
 #pragma unroll
-                    for (int e = 0; e < 8; e++) {
+                    for (int e = 0; e < 8; e++)
                         p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][qb][8 * half + e], C, -mc));
-                        ps += p[e];
-                    }
-                    u32x4 pk4 = {pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]), pack2<T>(p[6], p[7])};
+                    // pack to the 16-bit operand and sum exactly those rounded
+                    // weights into l, so O and l use identical P
+                    u32x4 pk4 = {Op<T>::cvt2(p[0], p[1]), Op<T>::cvt2(p[2], p[3]), Op<T>::cvt2(p[4], p[5]),
+                                 Op<T>::cvt2(p[6], p[7])};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) ps = Op<T>::sum2(pk4[e], ps);
                     pf[qb][2 * kb + half] = __builtin_bit_cast(v8, pk4);
                 }
             }
-            l[qb] = l[qb] * corr + ps;
-#pragma unroll
-            for (int db = 0; db < 4; db++) o[qb][db] *= corr;
+            l[qb] += ps;
         }
+    };
 
-        // O^T[db][qb] += V^T[32 db .. +32][chunk] . P^T[chunk][qb]
-        const uint16_t* pv = sV[buf] + fr * VROW + 8 * hi;
+    // O^T[db][qb] += V^T[32 db .. +32][chunk] . P^T[chunk][qb]
+    auto pv = [&](const int buf, PTile& pf) {
+        const uint16_t* pvp = sV[buf] + fr * VROW + 8 * hi;
 #pragma unroll
         for (int kc = 0; kc < 4; kc++) {
 #pragma unroll
             for (int db = 0; db < 4; db++) {
-                v8 vf = __builtin_bit_cast(v8, *(const u32x4*)(pv + 32 * db * VROW + 16 * kc));
+                v8 vf = __builtin_bit_cast(v8, *(const u32x4*)(pvp + 32 * db * VROW + 16 * kc));
 #pragma unroll
                 for (int qb = 0; qb < QB; qb++) o[qb][db] = Op<T>::mfma32(vf, pf[qb][kc], o[qb][db]);
             }
         }
+    };
 
-        if (tix + 1 < ntiles) sstore(buf ^ 1);
-        __syncthreads();
+    const int ntiles = (lkv + KT - 1) / KT;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+
+    STile s;
+    PTile pf;
+    if (!PS || w < NW / 2) {
+        // in-phase: S(j), softmax(j), PV(j)
+        for (int j = 0; j + 1 < ntiles; j++) {
+            gload((j + 1) * KT);
+            scores(j % NBUF, s);
+            softmax(s, pf, j * KT, false);
+            pv(j % NBUF, pf);
+            sstore((j + 1) % NBUF);
+            __syncthreads();
+        }
+        const int jl = ntiles - 1;
+        scores(jl % NBUF, s);
+        softmax(s, pf, jl * KT, true);
+        pv(jl % NBUF, pf);
+    } else {
+        // half a tile behind: softmax(j-1), PV(j-1), S(j)
+        for (int j = 0; j + 1 < ntiles; j++) {
+            gload((j + 1) * KT);
+            if (j > 0) {
+                softmax(s, pf, (j - 1) * KT, false);
+                pv((j - 1) % NBUF, pf);
+            }
+            scores(j % NBUF, s);
+            sstore((j + 1) % NBUF);
+            __syncthreads();
+        }
+        const int jl = ntiles - 1;
+        if (jl > 0) {
+            softmax(s, pf, (jl - 1) * KT, false);
+            pv((jl - 1) % NBUF, pf);
+        }
+        scores(jl % NBUF, s);
+        softmax(s, pf, jl * KT, true);
+        pv(jl % NBUF, pf);
     }
 
     // out[q][h * 128 + d] = O^T[d][q] / l * 2 sigmoid(glog[q][h])
@@ -213,15 +263,26 @@ __device__ void attn_body(const LtxAttnArgs& a) {
 #pragma unroll
             for (int rg = 0; rg < 4; rg++) {
                 int d = 32 * db + 8 * rg + 4 * hi;
-                u32x2 pk2 = {pack2<T>(o[qb][db][4 * rg] * sc, o[qb][db][4 * rg + 1] * sc),
-                             pack2<T>(o[qb][db][4 * rg + 2] * sc, o[qb][db][4 * rg + 3] * sc)};
+                u32x2 pk2 = {Op<T>::cvt2(o[qb][db][4 * rg] * sc, o[qb][db][4 * rg + 1] * sc),
+                             Op<T>::cvt2(o[qb][db][4 * rg + 2] * sc, o[qb][db][4 * rg + 3] * sc)};
                 *(u32x2*)(out + (size_t)q * LTX_D + h * LTX_HD + d) = pk2;
             }
         }
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256, 1) ltx_attn_f16(const LtxAttnArgs a) { attn_body<_Float16, 2>(a); }
-extern "C" __global__ void __launch_bounds__(256, 1) ltx_attn_bf16(const LtxAttnArgs a) { attn_body<__bf16, 2>(a); }
-extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_f16_w8(const LtxAttnArgs a) { attn_body<_Float16, 1>(a); }
-extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_bf16_w8(const LtxAttnArgs a) { attn_body<__bf16, 1>(a); }
+#define ATTN_KERNEL(NAME, T, QB, FULL, NW, PS)                                                      \
+    extern "C" __global__ void __launch_bounds__(64 * NW, 1) NAME(const LtxAttnArgs a) {           \
+        attn_body<T, QB, FULL, NW, PS>(a);                                                          \
+    }
+
+ATTN_KERNEL(ltx_attn_f16, _Float16, 2, false, 4, false)
+ATTN_KERNEL(ltx_attn_bf16, __bf16, 2, false, 4, false)
+ATTN_KERNEL(ltx_attn_f16_w8, _Float16, 1, false, 8, false)
+ATTN_KERNEL(ltx_attn_bf16_w8, __bf16, 1, false, 8, false)
+ATTN_KERNEL(ltx_attn_f16_w8_full, _Float16, 1, true, 8, false)
+ATTN_KERNEL(ltx_attn_bf16_w8_full, __bf16, 1, true, 8, false)
+ATTN_KERNEL(ltx_attn_f16_ps, _Float16, 1, false, 8, true)
+ATTN_KERNEL(ltx_attn_bf16_ps, __bf16, 1, false, 8, true)
+ATTN_KERNEL(ltx_attn_f16_ps_full, _Float16, 1, true, 8, true)
+ATTN_KERNEL(ltx_attn_bf16_ps_full, __bf16, 1, true, 8, true)

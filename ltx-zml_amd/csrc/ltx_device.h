@@ -13,6 +13,9 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // Operand traits: the MFMA operand type (f16 or bf16), its 8-wide vector,
 // f32 -> 16-bit rounding (round-to-nearest-even) and the 32x32x16 MFMA.
@@ -32,6 +35,15 @@ struct Op<_Float16> {
     static __device__ __forceinline__ f32x16 mfma32(v8 a, v8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
     }
+    // two f32 -> packed pair, one v_cvt_pk_f16_f32 (round to nearest even)
+    static __device__ __forceinline__ uint32_t cvt2(float a, float b) {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+    }
+    // acc + lo + hi of a packed pair (v_dot2c_f32_f16 with (1, 1))
+    static __device__ __forceinline__ float sum2(uint32_t p, float acc) {
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p), (f16x2){(_Float16)1.0f, (_Float16)1.0f}, acc,
+                                      false);
+    }
 };
 
 template <>
@@ -46,6 +58,13 @@ struct Op<__bf16> {
     }
     static __device__ __forceinline__ f32x16 mfma32(v8 a, v8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint32_t cvt2(float a, float b) {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+    }
+    static __device__ __forceinline__ float sum2(uint32_t p, float acc) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p), (bf16x2){(__bf16)1.0f, (__bf16)1.0f},
+                                               acc, false);
     }
 };
 
