@@ -1,0 +1,255 @@
+// W8A16 GEMM for gfx950 with LDS-DMA staging: y[M][N] = A[M][K] . W[N][K]^T,
+// A f16 activations, W int8 with one f16 scale per 128 consecutive k
+// (ltx/block.zig:462-471), fused epilogues as in gemm_common.h. The scales
+// arrive as pairs: a.scales is u32 [K / 128][N], each word the f16 scale in
+// both halves (laid out once at upload).
+//
+// Workgroup: 8 waves (two per SIMD), output tile 256 x 256; wave w owns rows
+// 128 (w / 4) .. +127 and columns 64 (w % 4) .. +63 (4 x 2 blocks of 32 x 32,
+// v_mfma_f32_32x32x16_f16, f32 accumulate).
+//
+// K is walked in tiles of 64. Each tile's A (256 x 64 f16, 32 KB) and W
+// (256 x 64 int8, 16 KB) go straight from global memory into LDS with
+// global_load_lds_dwordx4 (no register staging) into one of three stages, two
+// tiles ahead of the tile being multiplied. The weight tile stays int8 in LDS:
+// every wave dequantises the fragments it reads (half the LDS bytes of an f16
+// tile, no second LDS pass).
+//
+// Dequantisation is exact: for u = q + 128 (the byte read as unsigned), the
+// f16 with bits 0x6400 | u is 1024 + u; subtracting 1152 gives q exactly and
+// one f16 multiply by the f16 scale rounds q * s once to nearest even — the
+// operand RNE16(q * s) that the register-staged kernels also feed the MFMA.
+//
+// LDS layout: A rows of 128 B (8 chunks of 8 k), chunk c of row r stored in
+// slot c ^ (r & 7); W rows of 64 B (4 chunks of 16 k), chunk c of row n in
+// slot c ^ ((n >> 2) & 3). The DMA writes 64 consecutive 16-byte slots per
+// instruction; each lane picks the global chunk that belongs in its slot.
+//
+// k order inside a tile: for MFMA step t (0..3), lanes 0-31 multiply
+// k = 8 t + 0..7 and lanes 32-63 k = 32 + 8 t + 0..7 (A and W alike), so a
+// lane's A operands for the whole tile are 64 contiguous bytes of its row and
+// its W operands 32 contiguous bytes.
+//
+// Synchronisation: waits are explicit (s_waitcnt vmcnt for this wave's DMA,
+// lgkmcnt for its LDS reads) followed by s_barrier. Each stage is its own
+// __shared__ object, so the compiler's alias tracking of LDS DMA sees that a
+// read of one stage does not depend on DMA into another and adds no
+// vmcnt(0) of its own. With PP, the two waves of a SIMD run half a tile
+// apart: while one multiplies, the other reads fragments, dequantises and
+// issues DMA.
+#pragma once
+#include "gemm_common.h"
+
+typedef __attribute__((address_space(3))) void* lds_vptr;
+
+// s_waitcnt immediates (vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+#define Q8_WAIT_VM(n) ((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
+#define Q8_WAIT_LGKM0 (15 | (3 << 14) | (7 << 4))
+
+__shared__ __attribute__((aligned(1024))) uint8_t q8_sa0[32768];
+__shared__ __attribute__((aligned(1024))) uint8_t q8_sa1[32768];
+__shared__ __attribute__((aligned(1024))) uint8_t q8_sa2[32768];
+__shared__ __attribute__((aligned(1024))) uint8_t q8_sb0[16384];
+__shared__ __attribute__((aligned(1024))) uint8_t q8_sb1[16384];
+__shared__ __attribute__((aligned(1024))) uint8_t q8_sb2[16384];
+
+template <int S>
+__device__ __forceinline__ uint8_t* q8_stage_a() {
+    return S == 0 ? q8_sa0 : S == 1 ? q8_sa1 : q8_sa2;
+}
+template <int S>
+__device__ __forceinline__ uint8_t* q8_stage_b() {
+    return S == 0 ? q8_sb0 : S == 1 ? q8_sb1 : q8_sb2;
+}
+
+// 8 int8 weights (two dwords of an LDS chunk) -> one f16x8 operand, times
+// the scale pair s2.
+__device__ __forceinline__ f16x8 q8_dequant8(uint32_t w0, uint32_t w1, f16x2 s2) {
+    const f16x2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    uint32_t o[4];
+#pragma unroll
+    for (int d = 0; d < 2; d++) {
+        const uint32_t x = (d ? w1 : w0) ^ 0x80808080u;
+        const f16x2 p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u));
+        const f16x2 p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u));
+        o[2 * d] = __builtin_bit_cast(uint32_t, (p0 - off) * s2);
+        o[2 * d + 1] = __builtin_bit_cast(uint32_t, (p1 - off) * s2);
+    }
+    return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
+}
+
+// Raw buffer descriptor word 3 for gfx9-family parts (untyped dword access).
+#define Q8_RSRC_W3 0x00020000
+
+template <int EPI, bool PP>
+struct Q8Gemm {
+    static constexpr int NI = 4, NJ = 2;
+    const LtxGemmArgs& a;
+    f32x16 acc[NI][NJ];
+    __amdgpu_buffer_rsrc_t ra_, rb_, rs_;  // A, W and scale-pair buffers
+    int g, nk, ng;
+    uint32_t ga[4], gb[2];  // per-lane byte offsets of this wave's DMA sources (k-tile 0)
+    int la, lb;             // this wave's DMA destinations within a stage (uniform)
+    uint32_t offa[4], offb[2];
+    uint32_t so;            // byte offset of the lane's first scale pair in group 0
+    f16x2 s2[NJ];
+
+    __device__ __forceinline__ Q8Gemm(const LtxGemmArgs& args) : a(args) {}
+
+    template <int S>
+    __device__ __forceinline__ void dma(int k) {
+        uint8_t* da = q8_stage_a<S>() + la;
+        uint8_t* db = q8_stage_b<S>() + lb;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_, (lds_vptr)(da + 1024 * i), 16, ga[i], k * 128, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_, (lds_vptr)(db + 1024 * i), 16, gb[i], k * 64, 0, 0);
+    }
+
+    __device__ __forceinline__ void wait_dma(bool more2) {
+        if (more2)
+            __builtin_amdgcn_s_waitcnt(Q8_WAIT_VM(6));
+        else
+            __builtin_amdgcn_s_waitcnt(Q8_WAIT_VM(0));
+    }
+
+    // One K-tile: tile k sits in stage S; DMA of tile k + 2 (when more2) goes
+    // to stage (S + 2) % 3, the stage tile k - 1 was read from.
+    template <int S>
+    __device__ __forceinline__ void step(int k, bool more2) {
+        const uint8_t* sa = q8_stage_a<S>();
+        const uint8_t* sb = q8_stage_b<S>();
+        u32x4 fa[NI][4], wb[NJ][2];
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int c = 0; c < 2; c++) wb[j][c] = *(const u32x4*)(sb + offb[c] + 2048 * j);
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) fa[i][t] = *(const u32x4*)(sa + offa[t] + 4096 * i);
+        // scale pairs of the next tile, issued before this step's DMA so the
+        // DMA wait below also covers them
+        uint32_t sn[NJ];
+        const int gnext = min((k + 1) >> 1, ng - 1) * a.N * 4;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) sn[j] = __builtin_amdgcn_raw_buffer_load_b32(rs_, so + 128 * j, gnext, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (more2) dma<(S + 2) % 3>(k + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        if (PP) {
+            __builtin_amdgcn_s_waitcnt(Q8_WAIT_LGKM0);
+            if (g == 1) wait_dma(more2);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            f16x8 fb[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const u32x4 w = wb[j][t >> 1];
+                fb[j] = (t & 1) ? q8_dequant8(w[2], w[3], s2[j]) : q8_dequant8(w[0], w[1], s2[j]);
+            }
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, fa[i][t]), fb[j],
+                                                                        acc[i][j], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (!PP || g == 0) wait_dma(more2);
+        __builtin_amdgcn_s_waitcnt(Q8_WAIT_LGKM0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < NJ; j++) s2[j] = __builtin_bit_cast(f16x2, sn[j]);
+    }
+
+    __device__ __forceinline__ void run() {
+        const int tid = threadIdx.x, lane = tid & 63;
+        const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+        g = w >> 2;
+        const int q = w & 3;
+        const TileIdx ti = tile_of(blockIdx.x, a.tiles_m, a.tiles_n);
+        const int m0 = ti.tm * 256, n0 = ti.tn * 256;
+        nk = a.K / 64;
+        ng = a.K / LTX_GROUP;
+        ra_ = __builtin_amdgcn_make_buffer_rsrc((void*)a.a, 0, (int)((uint32_t)a.M * (uint32_t)a.lda * 2u), Q8_RSRC_W3);
+        rb_ = __builtin_amdgcn_make_buffer_rsrc((void*)a.b, 0, (int)((uint32_t)a.N * (uint32_t)a.K), Q8_RSRC_W3);
+        rs_ = __builtin_amdgcn_make_buffer_rsrc((void*)a.scales, 0, (int)((uint32_t)ng * (uint32_t)a.N * 4u),
+                                                Q8_RSRC_W3);
+        // DMA sources. A: instruction i of wave w fills rows 8 (4 w + i) .. +7,
+        // 8 lanes a row; W: rows 16 (2 w + i) .. +15, 4 lanes a row.
+        {
+            const int r = lane >> 3, c = (lane & 7) ^ (r & 7);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int row = min(m0 + 8 * (4 * w + i) + r, a.M - 1);
+                ga[i] = (uint32_t)row * (uint32_t)a.lda * 2u + 16u * c;
+            }
+            const int nr = lane >> 2, nc = (lane & 3) ^ ((lane >> 4) & 3);
+#pragma unroll
+            for (int i = 0; i < 2; i++) gb[i] = (uint32_t)(n0 + 16 * (2 * w + i) + nr) * (uint32_t)a.K + 16u * nc;
+            la = 4096 * w;
+            lb = 2048 * w;
+        }
+        // fragment reads: A row 128 g + 32 i + lane % 32, chunks 4 h + t;
+        // W row 64 q + 32 j + lane % 32, chunks 2 h + c (h = lane / 32)
+        {
+            const int h = lane >> 5, r = lane & 31;
+#pragma unroll
+            for (int t = 0; t < 4; t++) offa[t] = (128 * g + r) * 128 + 16 * ((4 * h + t) ^ (r & 7));
+#pragma unroll
+            for (int c = 0; c < 2; c++) offb[c] = (64 * q + r) * 64 + 16 * ((2 * h + c) ^ ((r >> 2) & 3));
+            so = 4u * (uint32_t)(n0 + 64 * q + r);
+        }
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++) acc[i][j] = f32x16{0};
+
+        // scale pairs first: the wait for tile 0 below then covers them too
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            s2[j] = __builtin_bit_cast(f16x2, __builtin_amdgcn_raw_buffer_load_b32(rs_, so + 128 * j, 0, 0));
+        __builtin_amdgcn_sched_barrier(0);
+        dma<0>(0);
+        dma<1>(1);  // K is a multiple of 128: nk >= 2
+        wait_dma(true);
+        __builtin_amdgcn_s_barrier();
+        if (PP && g == 1) __builtin_amdgcn_s_barrier();
+        // Main loop: three tiles per trip, every one with a DMA two tiles
+        // ahead; the last 2 to 4 tiles follow unrolled.
+        const int trips = (nk - 2) / 3;
+        for (int it = 0; it < trips; it++) {
+            const int k = 3 * it;
+            step<0>(k, true);
+            step<1>(k + 1, true);
+            step<2>(k + 2, true);
+        }
+        {
+            const int k = 3 * trips;  // nk - k is 2, 3 or 4
+            step<0>(k, k + 2 < nk);
+            step<1>(k + 1, k + 3 < nk);
+            if (k + 2 < nk) step<2>(k + 2, k + 4 < nk);
+            if (k + 3 < nk) step<0>(k + 3, false);
+        }
+        if (PP && g == 0) __builtin_amdgcn_s_barrier();
+        gemm_epilogue<_Float16, EPI, NI, NJ>(a, acc, m0 + 128 * g + 4 * (lane >> 5), n0 + 64 * q + (lane & 31), n0);
+    }
+};
+
+#define Q8_GEMM_KERNEL(NAME, EPI_)                                                           \
+    extern "C" __global__ void __launch_bounds__(512, 1) NAME(const LtxGemmArgs a) {         \
+        Q8Gemm<EPI_, false> k(a);                                                            \
+        k.run();                                                                             \
+    }                                                                                        \
+    extern "C" __global__ void __launch_bounds__(512, 1) NAME##_pp(const LtxGemmArgs a) {    \
+        Q8Gemm<EPI_, true> k(a);                                                             \
+        k.run();                                                                             \
+    }

@@ -136,6 +136,17 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
     g.tiles_m = (M + 255) / 256;
     g.tiles_n = p.N / 256;
     char name[64];
+    // LDS-DMA int8 kernel: f16 operands, f16 scales, K a multiple of 128, and
+    // byte offsets of A and W within 31 bits (32-bit buffer offsets)
+    if (mode == LTX_MODE_F16 && p.q8 && p.scale_f16 && p.s2.p && c->gemm_q8 != 0 && p.K % 128 == 0 &&
+        (uint64_t)M * lda * 2 < (1ull << 31) && (uint64_t)p.N * p.K < (1ull << 31)) {
+        g.scales = p.s2.p;
+        std::snprintf(name, sizeof(name), "ltx_gemm_q8_%s%s",
+                      epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv",
+                      c->gemm_q8 == 2 ? "_pp" : "");
+        c->launch(name, g.tiles_m * g.tiles_n, 1, 1, 512, &g, st, label);
+        return;
+    }
     std::snprintf(name, sizeof(name), "ltx_gemm_%s_%s_%s%s", msuffix(mode), bk,
                   epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv",
                   c->gemm_waves == 8 ? "_w8" : "");
@@ -389,6 +400,14 @@ int ltx_op_linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* sca
                 ltx::gemm32(c, p, 0, N, (const float*)a, M, (float*)y, LTX_EPI_STORE, nullptr, ada, 0, gelu,
                             (hipStream_t)stream);
             } else {
+                if (mode == LTX_MODE_F16 && scale_f16 && c->gemm_q8 != 0 && N % 256 == 0) {
+                    // the LDS-DMA kernel reads scale pairs [K/128][N]
+                    const size_t n2 = (size_t)N * (K / LTX_GROUP);
+                    if (c->op_pairs.bytes < n2 * 4) c->op_pairs.alloc(n2 * 4);
+                    LtxPairArgs pa{(const uint16_t*)scales, (uint32_t*)c->op_pairs.p, N, K / LTX_GROUP};
+                    c->launch("ltx_scale_pairs", (unsigned)((n2 + 255) / 256), 1, 1, 256, &pa, (hipStream_t)stream);
+                    p.s2.p = c->op_pairs.p;
+                }
                 LtxGemmArgs g{};
                 g.out = y;
                 g.ldo = N;
@@ -397,10 +416,10 @@ int ltx_op_linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* sca
                 ltx::gemm16(c, mode, p, a, M, K, LTX_EPI_STORE, g, (hipStream_t)stream);
             }
         } catch (...) {
-            p.q.p = p.s.p = p.bias.p = nullptr;
+            p.q.p = p.s.p = p.s2.p = p.bias.p = nullptr;
             throw;
         }
-        p.q.p = p.s.p = p.bias.p = nullptr;
+        p.q.p = p.s.p = p.s2.p = p.bias.p = nullptr;
     })
 }
 

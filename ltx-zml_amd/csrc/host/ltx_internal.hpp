@@ -49,6 +49,7 @@ struct LtxProj {
     int scale_f16 = 0;
     ltx::DevBuf q;            // int8 [N][K]
     ltx::DevBuf s;            // [N][K/128] f32 or f16
+    ltx::DevBuf s2;           // f16 scales only: u32 [K/128][N], each the scale in both halves
     ltx::DevBuf w_bf16;       // bf16 [N][K] (base tensor)
     ltx::DevBuf w_f16;        // f16 copy of the base tensor (F16 mode, non-q8)
     ltx::DevBuf bias;         // f32 [N] (may be empty)
@@ -70,7 +71,9 @@ struct ltx_block_weights {
 
 struct ltx_ctx {
     int device = 0;
-    // kernel variants: waves per workgroup of the GEMM (4 or 8) and attention (4 or 8)
+    // kernel variants: int8 GEMM (0: register-staged, 1: LDS-DMA, 2: LDS-DMA ping-pong),
+    // waves per workgroup of the register-staged GEMM (4 or 8), attention schedule
+    int gemm_q8 = 2;
     int gemm_waves = 8;
     int attn_variant = 1;  // 0: 4 waves x 64 queries, 1: 8 waves x 32, 2: 8 waves, halves phase-shifted
     std::vector<hipModule_t> modules;
@@ -78,6 +81,7 @@ struct ltx_ctx {
     std::string err;
     // workspace
     ltx::DevBuf ws;
+    ltx::DevBuf op_pairs;  // scale pairs of the last ltx_op_linear_q8 call (f16 scales)
     size_t ws_T = 0, ws_S = 0;
     int ws_mode = -1;
     void* stage_ptr[LTX_ST_COUNT] = {};

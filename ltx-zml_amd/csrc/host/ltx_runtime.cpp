@@ -143,6 +143,8 @@ int ltx_init(int device, ltx_ctx** out) {
         c->device = device;
         // variant overrides (used for A/B timing): 4 or 8 waves per workgroup
         if (const char* e = std::getenv("LTX_GEMM_WAVES")) c->gemm_waves = std::atoi(e) == 4 ? 4 : 8;
+        if (const char* e = std::getenv("LTX_GEMM_Q8"))
+            c->gemm_q8 = std::strcmp(e, "reg") == 0 ? 0 : std::strcmp(e, "dma") == 0 ? 1 : 2;
         if (const char* e = std::getenv("LTX_ATTN_VARIANT"))
             c->attn_variant = std::strcmp(e, "w4") == 0 ? 0 : std::strcmp(e, "ps") == 0 ? 2 : 1;
         for (const unsigned char* co : {ltx_co_k_gemm, ltx_co_k_attn, ltx_co_k_norm, ltx_co_k_f32}) {
@@ -169,6 +171,7 @@ void ltx_destroy(ltx_ctx* c) {
     }
     for (auto e : c->ev_pool) (void)hipEventDestroy(e);
     c->ws.free_();
+    c->op_pairs.free_();
     for (hipModule_t m : c->modules) (void)hipModuleUnload(m);
     delete c;
 }

@@ -93,6 +93,13 @@ static void build_proj(LtxProj& p, const void* const* base, const int8_t* const*
         }
         h2d(p.q, q.data(), q.size());
         h2d(p.s, s.data(), s.size());
+        if (sf16) {  // f16 scales also as pairs (s | s << 16), u32 [G][N], for the LDS-DMA kernels
+            const uint16_t* s16 = (const uint16_t*)s.data();
+            std::vector<uint32_t> s2((size_t)G * p.N);
+            for (size_t n = 0; n < (size_t)p.N; n++)
+                for (size_t g = 0; g < G; g++) s2[g * p.N + n] = (uint32_t)s16[n * G + g] * 0x10001u;
+            h2d(p.s2, s2.data(), s2.size() * 4);
+        }
     } else {
         std::vector<uint16_t> w((size_t)p.N * K);
         size_t r = 0;
@@ -137,7 +144,7 @@ static void build_gate(LtxProj& p, const void* const* base, int wi) {
 }
 
 static uint64_t proj_bytes(const LtxProj& p) {
-    return p.q.bytes + p.s.bytes + p.w_bf16.bytes + p.w_f16.bytes + p.bias.bytes;
+    return p.q.bytes + p.s.bytes + p.s2.bytes + p.w_bf16.bytes + p.w_f16.bytes + p.bias.bytes;
 }
 
 ltx_block_weights* upload(ltx_ctx* c, const void* const* base, const int8_t* const* q8, const void* const* q8s, int sf16) {

@@ -11,36 +11,13 @@
 // byte), which is the single-rounding f32 value q * s of dq4
 // (ltx/block.zig:462-471), then rounded to the 16-bit operand type.
 // LDS rows are padded by 16 bytes.
-#include "ltx_device.h"
+#include "gemm_common.h"
+#include "gemm_q8.h"
 
 #define BM 256
 #define BN 256
 #define BK 64
 #define LDSW (BK + 8)  // 16-bit elements per padded LDS row
-#define GM 8           // M-tiles per rasterisation group
-
-struct TileIdx {
-    int tm, tn;
-};
-
-// Hardware places workgroup b on XCD b % 8. Hand each XCD a contiguous run of
-// the tile sequence, and walk that sequence in groups of GM M-tiles x all
-// N-tiles, so the ~32 workgroups resident on one XCD share A rows and B
-// columns in that XCD's L2.
-__device__ __forceinline__ TileIdx tile_of(int bid, int tiles_m, int tiles_n) {
-    int nt = tiles_m * tiles_n;
-    int t = bid;
-    if ((nt & 7) == 0) t = (bid & 7) * (nt >> 3) + (bid >> 3);
-    int gsz = GM * tiles_n;
-    int g = t / gsz, r = t - g * gsz;
-    int gm0 = g * GM;
-    int gcnt = min(GM, tiles_m - gm0);
-    TileIdx ti;
-    ti.tm = gm0 + r % gcnt;
-    ti.tn = r / gcnt;
-    return ti;
-}
-
 template <typename T, int BKIND, int NT>
 struct Stage {
     static constexpr int NA = BM * (BK / 8) / NT;    // 16-byte A chunks per thread
@@ -169,46 +146,8 @@ __device__ void gemm_body(const LtxGemmArgs& a) {
         if (more) frags(buf ^ 1, 0, 0);
     }
 
-    // Epilogue. acc[i][j][r] sits at row 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4
-    // and column 32 j + lane % 32 of this wave's sub-tile.
-    const int rb = m0 + wm * 128 + 4 * (lane >> 5);
-    const int cb = n0 + wn * WN + (lane & 31);
-#pragma unroll
-    for (int i = 0; i < NI; i++) {
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int m = rb + 32 * i + 8 * (r >> 2) + (r & 3);
-            if (m >= a.M) continue;
-            const float* gt = nullptr;
-            const float* gs = nullptr;
-            if (EPI == LTX_EPI_RESID_GATE) {  // ada row of the gate: sst[i] + tstab[tidx[m]][i]
-                gt = a.ada.tstab + ((size_t)a.ada.tidx[m] * 9 + a.igate) * LTX_D;
-                gs = a.ada.sst + (size_t)a.igate * LTX_D;
-            }
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                const int n = cb + 32 * j;
-                float v = acc[i][j][r] + (a.bias ? a.bias[n] : 0.0f);
-                if (EPI == LTX_EPI_STORE) {
-                    if (a.gelu) v = gelu_tanh(v);
-                    if (a.out_f32)
-                        ((float*)a.out)[(size_t)m * a.ldo + n] = v;
-                    else
-                        ((uint16_t*)a.out)[(size_t)m * a.ldo + n] = Op<T>::bits(v);
-                } else if (EPI == LTX_EPI_RESID_GATE) {
-                    size_t o = (size_t)m * a.ldo + n;
-                    ((float*)a.out)[o] = a.resid[o] + v * (gt[n] + gs[n]);
-                } else {  // QKV
-                    if (n0 < a.nsplit) {
-                        ((float*)a.out)[(size_t)m * a.nsplit + n] = v;
-                    } else {
-                        int c = n - a.nsplit;  // = h * 128 + d
-                        ((uint16_t*)a.out2)[(size_t)c * a.M + m] = Op<T>::bits(v);
-                    }
-                }
-            }
-        }
-    }
+    // acc[i][j][r]: row 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4, column 32 j + lane % 32
+    gemm_epilogue<T, EPI, NI, NJ>(a, acc, m0 + wm * 128 + 4 * (lane >> 5), n0 + wn * WN + (lane & 31), n0);
 }
 
 #define GEMM_KERNEL(NAME, T, BK_, EPI_)                                                        \
@@ -235,6 +174,12 @@ GEMM_KERNEL(ltx_gemm_bf16_i8f16_resid, __bf16, LTX_B_I8_F16S, LTX_EPI_RESID_GATE
 GEMM_KERNEL(ltx_gemm_bf16_i8f16_qkv, __bf16, LTX_B_I8_F16S, LTX_EPI_QKV)
 GEMM_KERNEL(ltx_gemm_bf16_w16_store, __bf16, LTX_B_W16, LTX_EPI_STORE)
 GEMM_KERNEL(ltx_gemm_bf16_w16_resid, __bf16, LTX_B_W16, LTX_EPI_RESID_GATE)
+
+// LDS-DMA W8A16 kernels (f16 operands, f16 scales): ltx_gemm_q8_{store,resid,qkv}
+// and the ping-pong variants with suffix _pp.
+Q8_GEMM_KERNEL(ltx_gemm_q8_store, LTX_EPI_STORE)
+Q8_GEMM_KERNEL(ltx_gemm_q8_resid, LTX_EPI_RESID_GATE)
+Q8_GEMM_KERNEL(ltx_gemm_q8_qkv, LTX_EPI_QKV)
 
 // Gate logits (ltx/block.zig:238, 526, 564): glog[t][h] = a[t] . gw[h] + gb[h].
 // One wave per 32 token rows: 256 MFMAs over K = 4096, operands straight

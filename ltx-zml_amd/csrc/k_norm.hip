@@ -195,3 +195,11 @@ __device__ void dequant_body(const LtxDequantArgs& a) {
 
 extern "C" __global__ void __launch_bounds__(256) ltx_dequant_f16(const LtxDequantArgs a) { dequant_body<_Float16>(a); }
 extern "C" __global__ void __launch_bounds__(256) ltx_dequant_bf16(const LtxDequantArgs a) { dequant_body<__bf16>(a); }
+
+// Scale pairs for the LDS-DMA int8 GEMM: out[g][n] = s[n][g] in both halves.
+extern "C" __global__ void __launch_bounds__(256) ltx_scale_pairs(const LtxPairArgs a) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.N * a.G) return;
+    const int g = i / a.N, n = i - g * a.N;
+    a.out[i] = (uint32_t)a.s[(size_t)n * a.G + g] * 0x10001u;
+}

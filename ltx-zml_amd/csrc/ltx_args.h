@@ -121,6 +121,14 @@ typedef struct {
     int scale_f16;
 } LtxDequantArgs;
 
+// f16 scales [N][G] -> scale pairs u32 [G][N] (s | s << 16) for the LDS-DMA
+// int8 GEMM.
+typedef struct {
+    const uint16_t* s;
+    uint32_t* out;
+    int N, G;
+} LtxPairArgs;
+
 // f32 reference-precision kernels (mode LTX_MODE_F32).
 typedef struct {
     const float* a;     // [M][K]

@@ -76,6 +76,8 @@ def _gemm_case(M, N, K, seed, scale_f16=False, t3=True):
     (300, 256, 4096, True, False, False),   # ragged M, GELU, 16-bit output
     (64, 768, 16384, False, True, True),    # long K, f16 scales
     (512, 1024, 1024, False, False, False),
+    (300, 512, 4096, True, False, True),    # f16 scales: ragged M, GELU, 16-bit output
+    (768, 1280, 2048, False, True, True),   # f16 scales: several M and N tiles
 ])
 def test_linear_q8(ctx, mode, M, N, K, gelu, out_f32, scale_f16):
     say(f"linear_q8 mode={mode} M={M} N={N} K={K} gelu={gelu} out_f32={out_f32} scale_f16={scale_f16}")
@@ -103,6 +105,52 @@ def test_linear_q8(ctx, mode, M, N, K, gelu, out_f32, scale_f16):
     tol_same = 1e-5 if out_f32 else (1e-3 if mode == "f16" else 6e-3)
     assert oracle.rel_rms(got, same_ops) <= tol_same
     assert oracle.rel_rms(got, exact_w) <= (1e-3 if mode == "f16" else 6e-3)
+
+
+def _onehot_case(ctx, M, N, K, seed):
+    """y = E . W^T with E[m][k] = (k == m mod K): every output is one weight
+    operand times 1, so y must equal the 16-bit operand RNE16(q * s) bit for
+    bit (one nonzero product, f32 accumulation)."""
+    rng = np.random.default_rng(seed)
+    q = rng.integers(-128, 128, size=(N, K), dtype=np.int16).astype(np.int8)
+    s = (10.0 ** rng.uniform(-4, -1, size=(N, K // 128))).astype(np.float16)
+    e = np.zeros((M, K), np.float32)
+    e[np.arange(M), np.arange(M) % K] = 1.0
+    dq, ds = torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda()
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    ctx.linear_q8(to16(e, torch.float16).cuda(), dq, ds, None, y, mode=rt.MODE_F16)
+    torch.cuda.synchronize()
+    exact = q.astype(np.float64) * np.repeat(s.astype(np.float64), 128, axis=1)
+    want = exact.astype(np.float16).astype(np.float32)[:, np.arange(M) % K].T
+    return y.cpu().numpy(), want
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 512, 1024), (300, 256, 256)])
+def test_linear_q8_onehot_exact(ctx, M, N, K):
+    say(f"linear_q8 one-hot f16 M={M} N={N} K={K}")
+    got, want = _onehot_case(ctx, M, N, K, seed=M + K)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("variant", ["reg", "dma"])
+def test_linear_q8_variants(monkeypatch, variant):
+    """The other int8 GEMM schedules (register staging, LDS-DMA without ping-pong):
+    the one-hot exactness check and an f16-scale GEMM against the oracle."""
+    say(f"linear_q8 variant={variant}")
+    monkeypatch.setenv("LTX_GEMM_Q8", variant)
+    c = rt.Context(0)
+    try:
+        got, want = _onehot_case(c, 1024, 512, 1024, seed=9)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        a, q, s, b = _gemm_case(300, 768, 4096, seed=11, scale_f16=True)
+        y = torch.empty((300, 768), dtype=torch.float32, device="cuda")
+        c.linear_q8(to16(a, torch.float16).cuda(), torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(),
+                    torch.from_numpy(b).cuda(), y, mode=rt.MODE_F16)
+        torch.cuda.synchronize()
+        want = f64(to16(a, torch.float16)) @ oracle.dequant(q, s).astype(np.float64).T + b
+        assert oracle.rel_rms(f64(y), want) <= 1e-3
+    finally:
+        c.close()
 
 
 def test_linear_q8_f32_mode(ctx):
