@@ -21,7 +21,8 @@
 // operand RNE16(q * s) that the register-staged kernels also feed the MFMA.
 //
 // LDS layout: A rows of 128 B (8 chunks of 8 k), chunk c of row r stored in
-// slot c ^ (r & 7); W rows of 64 B (4 chunks of 16 k), chunk c of row n in
+// slot c ^ ((r >> 1) & 7) (16 consecutive rows, one ds_read_b128 lane group,
+// then cover all 64 banks once); W rows of 64 B (4 chunks of 16 k), chunk c of row n in
 // slot c ^ ((n >> 2) & 3). The DMA writes 64 consecutive 16-byte slots per
 // instruction; each lane picks the global chunk that belongs in its slot.
 //
@@ -186,10 +187,11 @@ struct Q8Gemm {
         // DMA sources. A: instruction i of wave w fills rows 8 (4 w + i) .. +7,
         // 8 lanes a row; W: rows 16 (2 w + i) .. +15, 4 lanes a row.
         {
-            const int r = lane >> 3, c = (lane & 7) ^ (r & 7);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int row = min(m0 + 8 * (4 * w + i) + r, a.M - 1);
+                const int tr = 8 * (4 * w + i) + (lane >> 3);  // row within the tile
+                const int c = (lane & 7) ^ ((tr >> 1) & 7);
+                const int row = min(m0 + tr, a.M - 1);
                 ga[i] = (uint32_t)row * (uint32_t)a.lda * 2u + 16u * c;
             }
             const int nr = lane >> 2, nc = (lane & 3) ^ ((lane >> 4) & 3);
@@ -203,7 +205,7 @@ struct Q8Gemm {
         {
             const int h = lane >> 5, r = lane & 31;
 #pragma unroll
-            for (int t = 0; t < 4; t++) offa[t] = (128 * g + r) * 128 + 16 * ((4 * h + t) ^ (r & 7));
+            for (int t = 0; t < 4; t++) offa[t] = (128 * g + r) * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7));
 #pragma unroll
             for (int c = 0; c < 2; c++) offb[c] = (64 * q + r) * 64 + 16 * ((2 * h + c) ^ ((r >> 2) & 3));
             so = 4u * (uint32_t)(n0 + 64 * q + r);
