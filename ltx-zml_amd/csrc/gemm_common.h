@@ -70,3 +70,100 @@ __device__ __forceinline__ void gemm_epilogue(const LtxGemmArgs& a, const f32x16
         }
     }
 }
+
+// LDS-staged epilogue: the same outputs as gemm_epilogue, for one wave's
+// (32 NI) x (32 NJ) tile at rows mw.., columns nw... Each 32-row block is
+// written to a wave-private LDS patch [32][32 NJ + 8] f32 and read back so
+// that every global load and store moves 16 contiguous bytes: f32 rows 4
+// columns a lane, 16-bit rows 8 columns a lane, V^T columns 8 rows a lane.
+// The patch is only touched by this wave (LDS operations of a wave complete in
+// order), so no barrier is needed; the caller guarantees no other wave still
+// reads that LDS.
+template <typename T, int EPI, int NI, int NJ>
+__device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f32x16 (&acc)[NI][NJ], float* patch,
+                                                  int mw, int nw, int n0) {
+    constexpr int WN = 32 * NJ, LD = WN + 8;
+    const int lane = threadIdx.x & 63;
+    const bool vt = EPI == LTX_EPI_QKV && n0 >= a.nsplit;
+    const bool f32out = EPI != LTX_EPI_STORE || a.out_f32;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                patch[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * LD + 32 * j + (lane & 31)] = acc[i][j][r];
+        const int mb = mw + 32 * i;
+        if (vt) {
+            // V^T [c][m]: 4 lanes cover one column's 32 rows (64 contiguous bytes)
+            const int rg = lane & 3;
+#pragma unroll
+            for (int p = 0; p < WN / 16; p++) {
+                const int cc = 16 * p + (lane >> 2);
+                const int n = nw + cc, c = n - a.nsplit;
+                const float bn = a.bias ? a.bias[n] : 0.0f;
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = patch[(8 * rg + e) * LD + cc] + bn;
+                const int m = mb + 8 * rg;
+                uint16_t* dst = (uint16_t*)a.out2 + (size_t)c * a.M + m;
+                if ((a.M & 7) == 0 && m + 8 <= a.M) {
+                    *(u32x4*)dst = u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
+                                         pack2<T>(v[6], v[7])};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        if (m + e < a.M) dst[e] = Op<T>::bits(v[e]);
+                }
+            }
+        } else if (f32out) {
+            constexpr int LPR = WN / 4, RPP = 64 / LPR;  // lanes per row, rows per pass
+            const int c4 = 4 * (lane % LPR), r0 = lane / LPR;
+            const int n = nw + c4;
+            f32x4 bias = a.bias ? *(const f32x4*)(a.bias + n) : f32x4{0, 0, 0, 0};
+            f32x4 gs = {0, 0, 0, 0};
+            if (EPI == LTX_EPI_RESID_GATE) gs = *(const f32x4*)(a.ada.sst + (size_t)a.igate * LTX_D + n);
+#pragma unroll
+            for (int p = 0; p < 32 / RPP; p++) {
+                const int rr = r0 + RPP * p, m = mb + rr;
+                if (m >= a.M) continue;
+                f32x4 v = *(const f32x4*)(patch + rr * LD + c4) + bias;
+                if (EPI == LTX_EPI_STORE) {
+                    if (a.gelu) v = f32x4{gelu_tanh(v[0]), gelu_tanh(v[1]), gelu_tanh(v[2]), gelu_tanh(v[3])};
+                    *(f32x4*)((float*)a.out + (size_t)m * a.ldo + n) = v;
+                } else if (EPI == LTX_EPI_RESID_GATE) {
+                    const f32x4 gt =
+                        *(const f32x4*)(a.ada.tstab + ((size_t)a.ada.tidx[m] * 9 + a.igate) * LTX_D + n);
+                    const size_t o = (size_t)m * a.ldo + n;
+                    const f32x4 rs = *(const f32x4*)(a.resid + o);
+                    *(f32x4*)((float*)a.out + o) = rs + v * (gt + gs);
+                } else {  // q | k part of the fused QKV projection
+                    *(f32x4*)((float*)a.out + (size_t)m * a.nsplit + n) = v;
+                }
+            }
+        } else {  // 16-bit rows: 8 columns a lane
+            constexpr int LPR = WN / 8, RPP = 64 / LPR;
+            const int c8 = 8 * (lane % LPR), r0 = lane / LPR;
+            const int n = nw + c8;
+            f32x4 b0 = {0, 0, 0, 0}, b1 = {0, 0, 0, 0};
+            if (a.bias) {
+                b0 = *(const f32x4*)(a.bias + n);
+                b1 = *(const f32x4*)(a.bias + n + 4);
+            }
+#pragma unroll
+            for (int p = 0; p < 32 / RPP; p++) {
+                const int rr = r0 + RPP * p, m = mb + rr;
+                if (m >= a.M) continue;
+                f32x4 v0 = *(const f32x4*)(patch + rr * LD + c8) + b0;
+                f32x4 v1 = *(const f32x4*)(patch + rr * LD + c8 + 4) + b1;
+                if (a.gelu) {
+                    v0 = f32x4{gelu_tanh(v0[0]), gelu_tanh(v0[1]), gelu_tanh(v0[2]), gelu_tanh(v0[3])};
+                    v1 = f32x4{gelu_tanh(v1[0]), gelu_tanh(v1[1]), gelu_tanh(v1[2]), gelu_tanh(v1[3])};
+                }
+                *(u32x4*)((uint16_t*)a.out + (size_t)m * a.ldo + n) =
+                    u32x4{pack2<T>(v0[0], v0[1]), pack2<T>(v0[2], v0[3]), pack2<T>(v1[0], v1[1]),
+                          pack2<T>(v1[2], v1[3])};
+            }
+        }
+    }
+}

@@ -242,7 +242,10 @@ struct Q8Gemm {
             if (k + 3 < nk) step<0>(k + 3, false);
         }
         if (PP && g == 0) __builtin_amdgcn_s_barrier();
-        gemm_epilogue<_Float16, EPI, NI, NJ>(a, acc, m0 + 128 * g + 4 * (lane >> 5), n0 + 64 * q + (lane & 31), n0);
+        // Every wave has passed its last barrier: no stage is read or DMA'd any
+        // more, and each wave stages its epilogue in a private 9 KB patch.
+        uint8_t* patch = w < 3 ? q8_sa0 + 9216 * w : w < 6 ? q8_sa1 + 9216 * (w - 3) : q8_sa2 + 9216 * (w - 6);
+        gemm_epilogue_lds<_Float16, EPI, NI, NJ>(a, acc, (float*)patch, m0 + 128 * g, n0 + 64 * q, n0);
     }
 };
 

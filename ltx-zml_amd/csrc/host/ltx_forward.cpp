@@ -138,8 +138,11 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
     char name[64];
     // LDS-DMA int8 kernel: f16 operands, f16 scales, K a multiple of 128, and
     // byte offsets of A and W within 31 bits (32-bit buffer offsets)
+    auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
     if (mode == LTX_MODE_F16 && p.q8 && p.scale_f16 && p.s2.p && c->gemm_q8 != 0 && p.K % 128 == 0 &&
-        (uint64_t)M * lda * 2 < (1ull << 31) && (uint64_t)p.N * p.K < (1ull << 31)) {
+        (uint64_t)M * lda * 2 < (1ull << 31) && (uint64_t)p.N * p.K < (1ull << 31) && g.ldo % 8 == 0 &&
+        al16(g.out) && al16(g.out2) && al16(g.resid) && al16(g.bias) && al16(g.ada.tstab) && al16(g.ada.sst)) {
+        // (its epilogue moves 16-byte vectors: outputs, residual and bias 16-byte aligned)
         g.scales = p.s2.p;
         std::snprintf(name, sizeof(name), "ltx_gemm_q8_%s%s",
                       epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv",
