@@ -178,10 +178,26 @@ static void attn16(ltx_ctx* c, int mode, const void* q, const void* k, const voi
     a.lq = lq;
     a.lkv = lkv;
     a.scale_log2 = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;
-    const int v = c->attn_variant;
+    int v = c->attn_variant;
     a.q_tiles = (lq + 255) / 256;                    // 256 queries per workgroup
-    const bool full = v != 0 && lkv % 64 == 0;       // key length a whole number of 64-key tiles
     char name[48];
+    if (v == 4) {
+        if (lkv % 64 == 0 && lkv >= 128) {  // ping-pong kernel: whole 64-key tiles, at least two
+            std::snprintf(name, sizeof(name), "ltx_attn_%s_pp", msuffix(mode));
+            c->launch(name, a.q_tiles * LTX_H, 1, 1, 512, &a, st, label);
+            return;
+        }
+        v = 1;
+    }
+    if (v == 3) {
+        if (lkv % 32 == 0 && lkv >= 128) {  // software-pipelined kernel: whole 32-key tiles, at least four
+            std::snprintf(name, sizeof(name), "ltx_attn_%s_sp", msuffix(mode));
+            c->launch(name, a.q_tiles * LTX_H, 1, 1, 256, &a, st, label);
+            return;
+        }
+        v = 1;
+    }
+    const bool full = v != 0 && lkv % 64 == 0;       // key length a whole number of 64-key tiles
     std::snprintf(name, sizeof(name), "ltx_attn_%s%s%s", msuffix(mode), v == 0 ? "" : v == 1 ? "_w8" : "_ps",
                   full ? "_full" : "");
     c->launch(name, a.q_tiles * LTX_H, 1, 1, v == 0 ? 256 : 512, &a, st, label);

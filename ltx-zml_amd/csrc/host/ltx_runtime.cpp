@@ -146,7 +146,11 @@ int ltx_init(int device, ltx_ctx** out) {
         if (const char* e = std::getenv("LTX_GEMM_Q8"))
             c->gemm_q8 = std::strcmp(e, "reg") == 0 ? 0 : std::strcmp(e, "dma") == 0 ? 1 : 2;
         if (const char* e = std::getenv("LTX_ATTN_VARIANT"))
-            c->attn_variant = std::strcmp(e, "w4") == 0 ? 0 : std::strcmp(e, "ps") == 0 ? 2 : 1;
+            c->attn_variant = std::strcmp(e, "w4") == 0   ? 0
+                              : std::strcmp(e, "ps") == 0 ? 2
+                              : std::strcmp(e, "sp") == 0 ? 3
+                              : std::strcmp(e, "pp") == 0 ? 4
+                                                          : 1;
         for (const unsigned char* co : {ltx_co_k_gemm, ltx_co_k_attn, ltx_co_k_norm, ltx_co_k_f32}) {
             hipModule_t m;
             HIPC(hipModuleLoadData(&m, co));

@@ -170,7 +170,9 @@ def _heads(x, L):  # [L, D] -> [H, L, 128]
 
 @pytest.mark.parametrize("mode", ["f16", "bf16"])
 @pytest.mark.parametrize("lq,lkv,gated", [(256, 256, True), (300, 200, True), (256, 32, False), (512, 1024, True),
-                                          (64, 77, True)])
+                                          (64, 77, True),
+                                          # pipelined kernel (whole 32-key tiles, >= 4): shortest loop, tails
+                                          (100, 128, True), (300, 160, True), (256, 480, False)])
 def test_attention(ctx, mode, lq, lkv, gated):
     say(f"attention mode={mode} lq={lq} lkv={lkv} gated={gated}")
     m, dt = MODES[mode]
@@ -212,11 +214,13 @@ def test_attention_f32_mode(ctx):
     assert oracle.rel_rms(f64(out), want) <= 1e-5
 
 
-def test_attention_special_cases(ctx):
-    """Identical keys -> mean of V; one dominant key -> that V row."""
-    say("attention special cases f16")
+@pytest.mark.parametrize("lkv,dom", [(96, 37), (160, 130)])
+def test_attention_special_cases(ctx, lkv, dom):
+    """Identical keys -> mean of V; one dominant key -> that V row (placed
+    past the first tiles, so the running max must move and rescale O)."""
+    say(f"attention special cases f16 lkv={lkv} dominant key={dom}")
     rng = np.random.default_rng(12)
-    lq, lkv = 64, 96
+    lq = 64
     q = rng.standard_normal((lq, 4096)).astype(np.float32)
     k = np.tile(rng.standard_normal((1, 4096)).astype(np.float32), (lkv, 1))
     v = rng.standard_normal((lkv, 4096)).astype(np.float32)
@@ -231,9 +235,35 @@ def test_attention_special_cases(ctx):
     # dominant key: key 37 equals 8 * q-direction for every head -> softmax ~ one-hot
     k2 = rng.standard_normal((lkv, 4096)).astype(np.float32) * 0.01
     qq = np.tile(rng.standard_normal((1, 4096)).astype(np.float32), (lq, 1))
-    k2[37] = qq[0] * 4.0
+    k2[dom] = qq[0] * 4.0
     args2 = [to16(_heads(qq, lq), dt).cuda(), to16(_heads(k2, lkv), dt).cuda(), args[2]]
     ctx.attention(*args2, None, out, lq, lkv, mode=rt.MODE_F16)
     torch.cuda.synchronize()
-    v37 = f64(args[2]).transpose(2, 0, 1).reshape(lkv, 4096)[37]
-    assert np.abs(f64(out) - v37[None, :]).max() < 5e-3
+    vd = f64(args[2]).transpose(2, 0, 1).reshape(lkv, 4096)[dom]
+    assert np.abs(f64(out) - vd[None, :]).max() < 5e-3
+
+
+@pytest.mark.parametrize("variant", ["w8", "w4", "sp", "pp"])
+def test_attention_variants(monkeypatch, variant):
+    """Each attention schedule against the dense f64 oracle on one case."""
+    say(f"attention variant={variant} lq=384 lkv=2048")
+    monkeypatch.setenv("LTX_ATTN_VARIANT", variant)
+    c = rt.Context(0)
+    try:
+        rng = np.random.default_rng(21)
+        lq, lkv = 384, 2048
+        q, k, v = (rng.standard_normal((n, 4096)).astype(np.float32) for n in (lq, lkv, lkv))
+        glog = rng.standard_normal((lq, 32)).astype(np.float32)
+        dt = torch.float16
+        dq, dk = to16(_heads(q, lq), dt).cuda(), to16(_heads(k, lkv), dt).cuda()
+        dv = to16(np.ascontiguousarray(v.reshape(lkv, 32, 128).transpose(1, 2, 0)), dt).cuda()
+        out = torch.empty((lq, 4096), dtype=dt, device="cuda")
+        c.attention(dq, dk, dv, torch.from_numpy(glog).cuda(), out, lq, lkv, mode=rt.MODE_F16)
+        torch.cuda.synchronize()
+        want = oracle.sdpa(f64(dq).transpose(1, 0, 2).reshape(lq, 4096), f64(dk).transpose(1, 0, 2).reshape(lkv, 4096),
+                           f64(dv).transpose(2, 0, 1).reshape(lkv, 4096), chunk=0)
+        g = 2.0 / (1.0 + np.exp(-glog.astype(np.float64)))
+        want = (want.reshape(lq, 32, 128) * g[:, :, None]).reshape(lq, 4096)
+        assert oracle.rel_rms(f64(out), want) <= 2e-3
+    finally:
+        c.close()
