@@ -140,8 +140,19 @@ struct Q8Gemm {
         __builtin_amdgcn_sched_barrier(0);
         if (more2) dma<(S + 2) % 3>(k + 2);
         __builtin_amdgcn_sched_barrier(0);
+        // ping-pong: the first DQ k-steps are dequantised in this (memory)
+        // phase, so the MFMA phase opens with MFMAs; the rest interleave with it
+        constexpr int DQ = PP ? 2 : 0;
+        f16x8 fb0[DQ > 0 ? DQ : 1][NJ];
         if (PP) {
             __builtin_amdgcn_s_waitcnt(Q8_WAIT_LGKM0);
+#pragma unroll
+            for (int t = 0; t < DQ; t++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) {
+                    const u32x4 w = wb[j][t >> 1];
+                    fb0[t][j] = (t & 1) ? q8_dequant8(w[2], w[3], s2[j]) : q8_dequant8(w[0], w[1], s2[j]);
+                }
             if (g == 1) wait_dma(more2);
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_barrier();
@@ -153,7 +164,10 @@ struct Q8Gemm {
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
                 const u32x4 w = wb[j][t >> 1];
-                fb[j] = (t & 1) ? q8_dequant8(w[2], w[3], s2[j]) : q8_dequant8(w[0], w[1], s2[j]);
+                if (t < DQ)
+                    fb[j] = fb0[t < DQ ? t : 0][j];
+                else
+                    fb[j] = (t & 1) ? q8_dequant8(w[2], w[3], s2[j]) : q8_dequant8(w[0], w[1], s2[j]);
             }
 #pragma unroll
             for (int i = 0; i < NI; i++)
