@@ -754,23 +754,9 @@ struct AttnPP {
         }
     }
 
-    // softmax phase: S^T accumulators -> P^T operands; the output rescale
-    // for a moving max is applied here, after PV(t-1) and before PV(t)
-    __device__ __forceinline__ void softmax() {
-        float mx = s[0][0];
-#pragma unroll
-        for (int r = 1; r < 16; r++) mx = fmaxf(mx, s[0][r]);
-#pragma unroll
-        for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[1][r]);
-        mx = asp_xhalf_max(mx);
-        if (__builtin_amdgcn_ballot_w64(mx > m + RESCALE_LOG2 / C) != 0) {
-            const float mn = fmaxf(m, mx);
-            const float corr = __builtin_amdgcn_exp2f((m - mn) * C);
-            m = mn;
-            l *= corr;
-#pragma unroll
-            for (int db = 0; db < 4; db++) o[db] *= corr;
-        }
+    // P^T operands and their row sum for the running max m (exp2 of
+    // s C - m C, the 1/sqrt(128) scale folded into C)
+    __device__ __forceinline__ float exps() {
         const float mc = m * C;
         float ps = 0.f;
 #pragma unroll
@@ -784,6 +770,32 @@ struct AttnPP {
 #pragma unroll
             for (int e = 0; e < 4; e++) ps = Op<T>::sum2(pk4[e], ps);
             pf[kc] = __builtin_bit_cast(v8, pk4);
+        }
+        return ps;
+    }
+
+    // softmax phase: S^T accumulators -> P^T operands. The weights are first
+    // formed with the running max; only if some lane's sum of its rounded
+    // weights exceeds 2^8 (a weight above 2^8, or an f16 overflow, which sums
+    // to inf) is the tile max taken, the max moved, the output and row sum
+    // rescaled (after PV(t-1), before PV(t)) and the weights formed again.
+    // The first tile always takes that path (m starts at -FLT_MAX).
+    __device__ __forceinline__ void softmax() {
+        float ps = exps();
+        if (__builtin_amdgcn_ballot_w64(!(ps <= 256.0f)) != 0) {
+            float mx = s[0][0];
+#pragma unroll
+            for (int r = 1; r < 16; r++) mx = fmaxf(mx, s[0][r]);
+#pragma unroll
+            for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[1][r]);
+            mx = asp_xhalf_max(mx);
+            const float mn = fmaxf(m, mx);
+            const float corr = __builtin_amdgcn_exp2f((m - mn) * C);
+            m = mn;
+            l *= corr;
+#pragma unroll
+            for (int db = 0; db < 4; db++) o[db] *= corr;
+            ps = exps();
         }
         l += ps;
     }
