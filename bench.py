@@ -31,7 +31,7 @@ PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
 # HBM bytes per self-attention launch from rocprofv3 FETCH_SIZE (x2.0, the
 # factor a 1 GiB copy calibrates) + WRITE_SIZE (x1.0), for the kernel as
 # built at that measurement (profiles/attn_self_t28672_f16_hbm_bytes.md).
-ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.520e9}
+ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.467e9}
 
 
 def flops(T: int, S: int) -> dict:
@@ -188,7 +188,7 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS, 4),
                      "traffic": ATTN_SELF_TRAFFIC.get((T, args.mode)),
-                     "kernel": "ltx_attn_" + args.mode + "_w8_full (self-attention, 4*H*T^2*HD = "
+                     "kernel": "ltx_attn_" + args.mode + "_pp (self-attention, 4*H*T^2*HD = "
                                f"{f['self_attn'] / 1e12:.3f} TFLOP per launch)"},
     }
     w.free()

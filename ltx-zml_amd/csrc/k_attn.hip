@@ -906,23 +906,37 @@ struct AttnPP {
             if (u + 2 <= nt) step<0, false>(u + 2);
         }
         if (g == 0) __builtin_amdgcn_s_barrier();
-        // out[q][h * 128 + d] = O^T[d][q] / l * 2 sigmoid(glog[q][h])
-        uint16_t* out = (uint16_t*)a.out;
-        const int hh = lane >> 5;
+        // out[q][h * 128 + d] = O^T[d][q] / l * 2 sigmoid(glog[q][h]), through
+        // a wave-private LDS patch [32 q][64 d] (row pitch 72 elements,
+        // 144 B) per half of d so that every global store is 16 contiguous
+        // bytes of a row.
+        // All waves have passed their last barrier: the stages are free.
+        const int hh = lane >> 5, r = lane & 31;
         const float lt = l + __shfl_xor(l, 32, 64);
-        const int q = q0 + (lane & 31);
-        if (q < lq) {
-            const float gg = a.glog ? 2.0f * sigmoid_f(a.glog[(size_t)q * LTX_H + h]) : 1.0f;
-            const float sc = gg / lt;
+        const int qr = q0 + r;
+        const float gg = (a.glog && qr < lq) ? 2.0f * sigmoid_f(a.glog[(size_t)qr * LTX_H + h]) : 1.0f;
+        const float sc = gg / lt;
+        uint16_t* patch = (uint16_t*)(w < 3 ? app_k0 + 4608 * w : w < 6 ? app_k1 + 4608 * (w - 3) : app_k2 + 4608 * (w - 6));
+        uint16_t* out = (uint16_t*)a.out;
 #pragma unroll
-            for (int db = 0; db < 4; db++) {
+        for (int half = 0; half < 2; half++) {
+#pragma unroll
+            for (int dbh = 0; dbh < 2; dbh++) {
+                const int db = 2 * half + dbh;
 #pragma unroll
                 for (int rg = 0; rg < 4; rg++) {
-                    const int d = 32 * db + 8 * rg + 4 * hh;
-                    const u32x2 pk2 = {Op<T>::cvt2(o[db][4 * rg] * sc, o[db][4 * rg + 1] * sc),
-                                       Op<T>::cvt2(o[db][4 * rg + 2] * sc, o[db][4 * rg + 3] * sc)};
-                    *(u32x2*)(out + (size_t)q * LTX_D + h * LTX_HD + d) = pk2;
+                    const int d = 32 * dbh + 8 * rg + 4 * hh;  // within this half
+                    *(u32x2*)(patch + r * 72 + d) =
+                        u32x2{Op<T>::cvt2(o[db][4 * rg] * sc, o[db][4 * rg + 1] * sc),
+                              Op<T>::cvt2(o[db][4 * rg + 2] * sc, o[db][4 * rg + 3] * sc)};
                 }
+            }
+#pragma unroll
+            for (int it = 0; it < 4; it++) {
+                const int row = 8 * it + (lane >> 3), c = lane & 7;  // 8 lanes x 16 B per row
+                const u32x4 v = *(const u32x4*)(patch + row * 72 + 8 * c);
+                const int q = q0 + row;
+                if (q < lq) *(u32x4*)(out + (size_t)q * LTX_D + h * LTX_HD + 64 * half + 8 * c) = v;
             }
         }
     }
