@@ -159,6 +159,63 @@ int ltx_profile_enable(ltx_ctx* ctx, int enable);
 int ltx_profile_read(ltx_ctx* ctx, const char* substr, double* total_ms, int* count);
 int ltx_profile_reset(ltx_ctx* ctx);
 
+/* ---- parts around the blocks (ltx/core_parts.zig) ---------------------- */
+
+#define LTX_IN_CH 128 /* latent channels (ltx/core_parts.zig:15) */
+
+typedef struct ltx_core_weights ltx_core_weights;
+
+/* Core tensors in CORE_SPECS order (ltx/core_parts.zig:53-72): bf16 bits
+ * [O][I] / [O], except fsst, f32 [2][4096]. */
+enum {
+    LTX_C_ADA_L1_W, LTX_C_ADA_L1_B, LTX_C_ADA_L2_W, LTX_C_ADA_L2_B, LTX_C_ADA_OUT_W, LTX_C_ADA_OUT_B,
+    LTX_C_PADA_L1_W, LTX_C_PADA_L1_B, LTX_C_PADA_L2_W, LTX_C_PADA_L2_B, LTX_C_PADA_OUT_W, LTX_C_PADA_OUT_B,
+    LTX_C_PAT_W, LTX_C_PAT_B, LTX_C_PO_W, LTX_C_PO_B, LTX_C_FSST, LTX_C_COUNT
+};
+
+/* Upload the core tensors from host memory (the role of loadCoreBufs,
+ * ltx/e2e_denoise.zig:73-84). Weights stay bf16; biases are widened to f32. */
+int ltx_core_weights_from_host(ltx_ctx* ctx, const void* const* tensors, ltx_core_weights** out);
+void ltx_core_weights_free(ltx_ctx* ctx, ltx_core_weights* cw);
+
+/* CoreParts.ts9r + emb + pts2r (ltx/core_parts.zig:112-141), f32:
+ *   t [K] raw timesteps (mask * sigma), sigma [1]   (device pointers)
+ *   tstab [K][9][4096], emb [K][4096] (embedded_timestep), pts2 [2][4096]. */
+int ltx_core_conditioning(ltx_ctx* ctx, const ltx_core_weights* cw, const float* t, int K, const float* sigma,
+                          float* tstab, float* emb, float* pts2, void* stream);
+/* CoreParts.patchify (ltx/core_parts.zig:143-145): latent [T][128] -> x [T][4096]. */
+int ltx_core_patchify(ltx_ctx* ctx, const ltx_core_weights* cw, const float* latent, int T, float* x, void* stream);
+/* CoreParts.tailFromEmb (ltx/core_parts.zig:147-166): LayerNorm, modulation
+ * by fsst + emb[tidx[t]], proj_out. x [T][4096] -> vel [T][128]. */
+int ltx_core_tail(ltx_ctx* ctx, const ltx_core_weights* cw, const float* x, const float* emb, const int32_t* tidx,
+                  int T, float* vel, void* stream);
+
+/* ---- distilled scheduler (ltx/scheduler.zig) ---------------------------- */
+
+/* SIGMAS_STAGE1 (stage 1, 9 values) or SIGMAS_STAGE2 (stage 2, 4 values),
+ * ltx/scheduler.zig:15-18. `out` may be NULL to read the count only. */
+int ltx_sched_sigmas(int stage, float* out, int* count);
+/* noiseInit (ltx/scheduler.zig:37-46) on device, bit-exact: latent [T][C],
+ * mask of token t = maskk[tidx[t]]. */
+int ltx_sched_noise_init(ltx_ctx* ctx, const float* clean, const float* noise, const float* maskk,
+                         const int32_t* tidx, int T, int C, float noise_scale, float* out, void* stream);
+/* toDenoised -> postProcess -> eulerStep (ltx/scheduler.zig:53-80) fused,
+ * bit-exact: ts of token t = tk[tidx[t]], mask maskk[tidx[t]]. out may
+ * equal x. */
+int ltx_sched_step(ltx_ctx* ctx, const float* x, const float* vel, const float* tk, const float* maskk,
+                   const int32_t* tidx, const float* clean, int T, int C, float sigma, float sigma_next, float* out,
+                   void* stream);
+
+/* The denoising loop (ltx/e2e_denoise.zig:218-336; one pass: ltx/e2e_prod.zig:302-430):
+ * per step, timesteps -> ts9r/emb/pts2r -> patchify -> every block ->
+ * tail -> scheduler step, with the latent [T][128] updated in place on the
+ * device. sigmas: host array of nsteps + 1 values. K distinct mask values
+ * maskk [K] (device), K < 64. blocks: nblocks resident block weights. */
+int ltx_denoise(ltx_ctx* ctx, const ltx_block_weights* const* blocks, int nblocks, const ltx_core_weights* cw,
+                float* latent, const float* clean, const float* maskk, const int32_t* tidx, int K,
+                const float* ctx_tokens, int S, const float* cos, const float* sin, int T, const float* sigmas,
+                int nsteps, int mode, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

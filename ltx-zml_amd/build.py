@@ -23,8 +23,8 @@ BUILD = PKG / "_build"
 LIB = PKG / "libltx_amd.so"
 INCLUDE = PKG.parent / "include"
 ROCM = pathlib.Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
-KERNELS = ["k_gemm", "k_attn", "k_norm", "k_f32"]
-HOST = ["ltx_runtime", "ltx_forward", "ltx_weights", "ltx_rope", "ltx_loader", "sha256"]
+KERNELS = ["k_gemm", "k_attn", "k_norm", "k_f32", "k_core"]
+HOST = ["ltx_runtime", "ltx_forward", "ltx_weights", "ltx_rope", "ltx_loader", "ltx_core", "sha256"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "--genco",

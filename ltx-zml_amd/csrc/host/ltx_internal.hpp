@@ -85,6 +85,9 @@ struct ltx_ctx {
     // workspace
     ltx::DevBuf ws;
     ltx::DevBuf op_pairs;  // scale pairs of the last ltx_op_linear_q8 call (f16 scales)
+    ltx::DevBuf core_ws;   // conditioning MLP rows
+    ltx::DevBuf tail_ws;   // normed rows of ltx_core_tail
+    ltx::DevBuf dn_ws;     // the denoising loop's activations
     size_t ws_T = 0, ws_S = 0;
     int ws_mode = -1;
     void* stage_ptr[LTX_ST_COUNT] = {};

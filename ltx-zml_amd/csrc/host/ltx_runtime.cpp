@@ -8,7 +8,7 @@
 
 // gfx950 code objects, embedded at build time (ltx_codeobjects.S).
 extern "C" {
-extern const unsigned char ltx_co_k_gemm[], ltx_co_k_attn[], ltx_co_k_norm[], ltx_co_k_f32[];
+extern const unsigned char ltx_co_k_gemm[], ltx_co_k_attn[], ltx_co_k_norm[], ltx_co_k_f32[], ltx_co_k_core[];
 }
 
 namespace ltx {
@@ -151,7 +151,7 @@ int ltx_init(int device, ltx_ctx** out) {
                               : std::strcmp(e, "sp") == 0 ? 3
                               : std::strcmp(e, "pp") == 0 ? 4
                                                           : 1;
-        for (const unsigned char* co : {ltx_co_k_gemm, ltx_co_k_attn, ltx_co_k_norm, ltx_co_k_f32}) {
+        for (const unsigned char* co : {ltx_co_k_gemm, ltx_co_k_attn, ltx_co_k_norm, ltx_co_k_f32, ltx_co_k_core}) {
             hipModule_t m;
             HIPC(hipModuleLoadData(&m, co));
             c->modules.push_back(m);
@@ -176,6 +176,9 @@ void ltx_destroy(ltx_ctx* c) {
     for (auto e : c->ev_pool) (void)hipEventDestroy(e);
     c->ws.free_();
     c->op_pairs.free_();
+    c->core_ws.free_();
+    c->tail_ws.free_();
+    c->dn_ws.free_();
     for (hipModule_t m : c->modules) (void)hipModuleUnload(m);
     delete c;
 }

@@ -164,6 +164,59 @@ typedef struct {
     int ldx;
 } LtxQkNorm32Args;
 
+// Parts around the blocks (ltx/core_parts.zig) and the scheduler
+// (ltx/scheduler.zig).
+typedef struct {
+    const float* t;     // [rows] timestep values
+    float* out;         // [rows][256]
+    int rows;
+} LtxSinArgs;
+
+typedef struct {
+    const float* x;
+    float* y;
+    size_t n;
+} LtxEltArgs;
+
+typedef struct {
+    const float* x;       // [T][D]
+    const float* fsst;    // [2][D] (shift row, scale row)
+    const float* emb;     // [K][D] embedded timestep per distinct t
+    const int32_t* tidx;  // [T]
+    float* y;             // [T][D]
+} LtxTailNormArgs;
+
+typedef struct {
+    const float* x;       // latent [T][stride]
+    const float* v;       // velocity [T][stride]
+    const float* clean;   // clean latent [T][stride]
+    const float* tk;      // [K] mask * sigma
+    const float* maskk;   // [K] mask values
+    const int32_t* tidx;  // [T]
+    float* y;
+    size_t n;             // T * stride
+    int stride;
+    float sigma, sigma_next;
+} LtxSchedArgs;
+
+typedef struct {
+    const float* clean;
+    const float* noise;
+    const float* maskk;
+    const int32_t* tidx;
+    float* y;
+    size_t n;
+    int stride;
+    float noise_scale;
+} LtxNoiseArgs;
+
+typedef struct {
+    const float* maskk;
+    float* tk;
+    int K;
+    float sigma;
+} LtxTimestepArgs;
+
 #ifdef __cplusplus
 }
 #endif

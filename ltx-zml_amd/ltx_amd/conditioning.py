@@ -31,8 +31,56 @@ def _rng(seed: int, name: str) -> np.random.Generator:
     return np.random.default_rng([seed, zlib.crc32(name.encode())])
 
 
+def _bits(seed: int, name: str, shape) -> np.ndarray:
+    return bf16_bits(_rng(seed, name).standard_normal(shape, dtype=np.float32) * 0.02)
+
+
 def _w(seed: int, name: str, shape) -> np.ndarray:
-    return bf16_to_f32(bf16_bits(_rng(seed, name).standard_normal(shape, dtype=np.float32) * 0.02))
+    return bf16_to_f32(_bits(seed, name, shape))
+
+
+# The core tensors in CORE_SPECS order (ltx/core_parts.zig:53-72): name,
+# shape. All bf16 except the f32 scale_shift_table "fsst".
+IN_CH = 128
+CORE_SPECS = [
+    ("ada_l1_w", (D, TE)), ("ada_l1_b", (D,)), ("ada_l2_w", (D, D)), ("ada_l2_b", (D,)),
+    ("ada_out_w", (9 * D, D)), ("ada_out_b", (9 * D,)),
+    ("pada_l1_w", (D, TE)), ("pada_l1_b", (D,)), ("pada_l2_w", (D, D)), ("pada_l2_b", (D,)),
+    ("pada_out_w", (2 * D, D)), ("pada_out_b", (2 * D,)),
+    ("pat_w", (D, IN_CH)), ("pat_b", (D,)), ("po_w", (IN_CH, D)), ("po_b", (IN_CH,)),
+    ("fsst", (2, D)),
+]
+CORE_FIELDS = [n for n, _ in CORE_SPECS]
+
+
+def make_core(seed: int = 7) -> dict:
+    """Seeded core tensors: bf16 bits (uint16) ~ N(0, 0.02) for the linear
+    layers, the same draws ``tables`` uses for the conditioning MLPs; fsst
+    f32 ~ N(0, 1) / sqrt(D)."""
+    out = {}
+    for name, shape in CORE_SPECS:
+        if name == "fsst":
+            g = _rng(seed, name)
+            out[name] = (g.standard_normal(shape, dtype=np.float32) / np.float32(np.sqrt(D))).astype(np.float32)
+        else:
+            out[name] = _bits(seed, name, shape)
+    return out
+
+
+def mask_rows(T: int, striped: bool = True) -> tuple[np.ndarray, np.ndarray]:
+    """Distinct denoise-mask values [K] f32 and the per-token row index
+    tidx [T] i32. Striped: the production pass's mask (ltx/e2e_prod.zig:
+    218-229), 0 for the first T/7 tokens, 0.5 for the next T/7, 1 for the
+    rest; else one row of 1."""
+    if striped:
+        mask = np.array([0.0, 0.5, 1.0], dtype=np.float32)
+        tidx = np.full(T, 2, dtype=np.int32)
+        tidx[: T // 7] = 0
+        tidx[T // 7: 2 * T // 7] = 1
+    else:
+        mask = np.array([1.0], dtype=np.float32)
+        tidx = np.zeros(T, dtype=np.int32)
+    return mask, tidx
 
 
 def sinusoid(t: np.ndarray) -> np.ndarray:
@@ -69,14 +117,7 @@ def tables(sigma: float, T: int, seed: int = 7, striped: bool = True):
     if seed not in _CACHE:
         _CACHE[seed] = _mlp_tables(seed)
     w = _CACHE[seed]
-    if striped:
-        mask = np.array([0.0, 0.5, 1.0], dtype=np.float32)
-        tidx = np.full(T, 2, dtype=np.int32)
-        tidx[: T // 7] = 0
-        tidx[T // 7: 2 * T // 7] = 1
-    else:
-        mask = np.array([1.0], dtype=np.float32)
-        tidx = np.zeros(T, dtype=np.int32)
+    mask, tidx = mask_rows(T, striped)
     t = (mask * np.float32(sigma)).astype(np.float32)
     e = sinusoid(t)
     h = _silu(e @ w["ada_l1_w"].T + w["ada_l1_b"])

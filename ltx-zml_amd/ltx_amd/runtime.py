@@ -74,6 +74,16 @@ def lib() -> C.CDLL:
         "ltx_ring_destroy": (None, [vp]),
         "ltx_loader_last_error": (C.c_char_p, []),
         "ltx_sha256_hex": (i32, [vp, u64, C.c_char_p]),
+        "ltx_core_weights_from_host": (i32, [vp, C.POINTER(vp), C.POINTER(vp)]),
+        "ltx_core_weights_free": (None, [vp, vp]),
+        "ltx_core_conditioning": (i32, [vp, vp, vp, i32, vp, vp, vp, vp, vp]),
+        "ltx_core_patchify": (i32, [vp, vp, vp, i32, vp, vp]),
+        "ltx_core_tail": (i32, [vp, vp, vp, vp, vp, i32, vp, vp]),
+        "ltx_sched_sigmas": (i32, [i32, vp, C.POINTER(i32)]),
+        "ltx_sched_noise_init": (i32, [vp, vp, vp, vp, vp, i32, i32, C.c_float, vp, vp]),
+        "ltx_sched_step": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i32, C.c_float, C.c_float, vp, vp]),
+        "ltx_denoise": (i32, [vp, C.POINTER(vp), i32, vp, vp, vp, vp, vp, i32, vp, i32, vp, vp, i32, vp, i32, i32,
+                              vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -107,6 +117,34 @@ def sha256_hex(data: bytes) -> str:
     out = C.create_string_buffer(65)
     lib().ltx_sha256_hex(data, len(data), out)
     return out.value.decode()
+
+
+def sched_sigmas(stage: int = 1) -> np.ndarray:
+    """The distilled sigma list of a stage (ltx/scheduler.zig:15-18)."""
+    n = C.c_int()
+    if not lib().ltx_sched_sigmas(stage, None, C.byref(n)):
+        raise LtxError(lib().ltx_last_error(None).decode())
+    out = np.empty(n.value, np.float32)
+    lib().ltx_sched_sigmas(stage, out.ctypes.data, C.byref(n))
+    return out
+
+
+class CoreWeights:
+    """Device copy of the parts around the blocks (ltx/core_parts.zig:86-104)."""
+
+    def __init__(self, ctx: "Context", handle: int):
+        self.ctx, self.handle = ctx, handle
+
+    def free(self):
+        if self.handle:
+            lib().ltx_core_weights_free(self.ctx.handle, self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 class Weights:
@@ -213,6 +251,62 @@ class Context:
         st = stream.cuda_stream if stream is not None else _current_stream()
         self._check(lib().ltx_op_dequant(self.handle, _ptr(q), _ptr(s), int(s.dtype == torch.float16), N, K,
                                          _ptr(out32), _ptr(out16), mode, st), "ltx_op_dequant")
+
+    # ---- parts around the blocks and the scheduler ----
+    def upload_core(self, tensors: dict) -> CoreWeights:
+        """tensors: field -> numpy array in CORE_SPECS order (bf16 bits as
+        uint16, fsst f32), e.g. conditioning.make_core()."""
+        from .conditioning import CORE_FIELDS
+        arrs = [np.ascontiguousarray(tensors[f]) for f in CORE_FIELDS]
+        ptrs = (C.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+        h = C.c_void_p()
+        self._check(lib().ltx_core_weights_from_host(self.handle, ptrs, C.byref(h)), "ltx_core_weights_from_host")
+        return CoreWeights(self, h.value)
+
+    def conditioning(self, cw: CoreWeights, t, sigma, tstab, emb, pts2, stream=None):
+        """t [K] f32, sigma [1] f32 (device) -> tstab [K, 9, D], emb [K, D], pts2 [2, D]."""
+        st = stream.cuda_stream if stream is not None else _current_stream()
+        self._check(lib().ltx_core_conditioning(self.handle, cw.handle, _ptr(t), t.shape[0], _ptr(sigma), _ptr(tstab),
+                                                _ptr(emb), _ptr(pts2), st), "ltx_core_conditioning")
+
+    def patchify(self, cw: CoreWeights, latent, x, stream=None):
+        st = stream.cuda_stream if stream is not None else _current_stream()
+        self._check(lib().ltx_core_patchify(self.handle, cw.handle, _ptr(latent), latent.shape[0], _ptr(x), st),
+                    "ltx_core_patchify")
+        return x
+
+    def tail(self, cw: CoreWeights, x, emb, tidx, vel, stream=None):
+        st = stream.cuda_stream if stream is not None else _current_stream()
+        self._check(lib().ltx_core_tail(self.handle, cw.handle, _ptr(x), _ptr(emb), _ptr(tidx), x.shape[0], _ptr(vel),
+                                        st), "ltx_core_tail")
+        return vel
+
+    def noise_init(self, clean, noise, maskk, tidx, noise_scale: float, out, stream=None):
+        T, Cc = clean.shape
+        st = stream.cuda_stream if stream is not None else _current_stream()
+        self._check(lib().ltx_sched_noise_init(self.handle, _ptr(clean), _ptr(noise), _ptr(maskk), _ptr(tidx), T, Cc,
+                                               float(noise_scale), _ptr(out), st), "ltx_sched_noise_init")
+        return out
+
+    def sched_step(self, x, vel, tk, maskk, tidx, clean, sigma: float, sigma_next: float, out, stream=None):
+        T, Cc = x.shape
+        st = stream.cuda_stream if stream is not None else _current_stream()
+        self._check(lib().ltx_sched_step(self.handle, _ptr(x), _ptr(vel), _ptr(tk), _ptr(maskk), _ptr(tidx),
+                                         _ptr(clean), T, Cc, float(sigma), float(sigma_next), _ptr(out), st),
+                    "ltx_sched_step")
+        return out
+
+    def denoise(self, blocks: list, cw: CoreWeights, latent, clean, maskk, tidx, ctx, cos, sin, sigmas,
+                mode: int = MODE_F16, stream=None):
+        """Runs len(sigmas) - 1 steps over the resident blocks; latent [T, 128]
+        is updated in place."""
+        sig = np.ascontiguousarray(sigmas, np.float32)
+        hs = (C.c_void_p * len(blocks))(*[b.handle for b in blocks])
+        st = stream.cuda_stream if stream is not None else _current_stream()
+        self._check(lib().ltx_denoise(self.handle, hs, len(blocks), cw.handle, _ptr(latent), _ptr(clean), _ptr(maskk),
+                                      _ptr(tidx), maskk.shape[0], _ptr(ctx), ctx.shape[0], _ptr(cos), _ptr(sin),
+                                      latent.shape[0], sig.ctypes.data, len(sig) - 1, mode, st), "ltx_denoise")
+        return latent
 
     # ---- profiling ----
     def profile(self, enable: bool):

@@ -279,3 +279,189 @@ def rel_rms(got, want) -> float:
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     return float(np.sqrt(((got - want) ** 2).sum() / ((want ** 2).sum() + 1e-300)))
+
+
+# ---- parts around the blocks (ltx/core_parts.zig), numpy -------------------
+# The sinusoid is f32 as in the reference (ltx/core_parts.zig:37-49: the
+# embedding is computed in f32 even under the f64 torch oracle); everything
+# after it is f64. Core tensors are a dict field -> array in CORE_SPECS order
+# (bf16 bits as uint16, fsst f32).
+
+CORE_EPS = 1e-6
+TE, HALF, IN_CH = 256, 128, 128
+
+
+def core_sinusoid(t) -> np.ndarray:
+    """ltx/core_parts.zig:42-49: freqs = exp(arange(128) * f32(-ln(1e4)/128)),
+    arg = (t * 1000) * freqs, [cos(arg) | sin(arg)], all f32."""
+    t = np.asarray(t, np.float32).reshape(-1, 1)
+    idx = np.arange(HALF, dtype=np.float32)
+    freqs = np.exp(idx * np.float32(-np.log(1e4) / HALF))
+    arg = (t * np.float32(1000.0)) * freqs[None, :]
+    return np.concatenate([np.cos(arg), np.sin(arg)], axis=1).astype(np.float32)
+
+
+def core_lin(x, cw: dict, name: str) -> np.ndarray:
+    """lin (ltx/block.zig:22-26): x . f32(W)^T + f32(b), in f64."""
+    return np.asarray(x, np.float64) @ _bf(cw[name + "_w"]).T + _bf(cw[name + "_b"])
+
+
+def core_silu(x):
+    return x / (1.0 + np.exp(-x))
+
+
+def core_emb(cw: dict, t) -> np.ndarray:
+    """embedded_timestep [K, D] (ltx/core_parts.zig:115-117)."""
+    return core_lin(core_silu(core_lin(core_sinusoid(t), cw, "ada_l1")), cw, "ada_l2")
+
+
+def core_ts9r(cw: dict, t) -> np.ndarray:
+    """ts9r [K, 9, D] (ltx/core_parts.zig:119-136)."""
+    ts9 = core_lin(core_silu(core_emb(cw, t)), cw, "ada_out")
+    return ts9.reshape(-1, 9, D)
+
+
+def core_pts2r(cw: dict, sigma: float) -> np.ndarray:
+    """pts2r [2, D] from scalar sigma (ltx/core_parts.zig:124-141)."""
+    e = core_lin(core_silu(core_lin(core_sinusoid([sigma]), cw, "pada_l1")), cw, "pada_l2")
+    return core_lin(core_silu(e), cw, "pada_out").reshape(2, D)
+
+
+def core_patchify(cw: dict, latent) -> np.ndarray:
+    """ltx/core_parts.zig:143-145: [T, 128] -> [T, D]."""
+    return core_lin(latent, cw, "pat")
+
+
+def core_layernorm(x) -> np.ndarray:
+    """LayerNorm without weight, biased variance, eps 1e-6 (ltx/core_parts.zig:30-35)."""
+    x = np.asarray(x, np.float64)
+    c = x - x.mean(-1, keepdims=True)
+    return c / np.sqrt((c * c).mean(-1, keepdims=True) + CORE_EPS)
+
+
+def core_tail_from_emb(cw: dict, x, e_tok, wrong_norm: bool = False) -> np.ndarray:
+    """tailFrom (ltx/core_parts.zig:147-166): shift = fsst[0] + e,
+    scale = fsst[1] + e, proj_out(norm(x) * (1 + scale) + shift). e_tok is
+    the per-token embedded_timestep [T, D]. wrong_norm: the reference's
+    RMS-norm control (ltx/core_parts.zig:175-180)."""
+    x = np.asarray(x, np.float64)
+    fsst = np.asarray(cw["fsst"], np.float64)
+    e = np.asarray(e_tok, np.float64)
+    n = x / np.sqrt((x * x).mean(-1, keepdims=True) + CORE_EPS) if wrong_norm else core_layernorm(x)
+    return core_lin(n * (1.0 + (fsst[1] + e)) + (fsst[0] + e), cw, "po")
+
+
+# ---- distilled scheduler (ltx/scheduler.zig), exact f32 ---------------------
+# numpy evaluates each f32 operation with one rounding and never contracts,
+# which is the reference's operation order; the lerp's fused multiply-add is
+# emulated exactly (fma_f32).
+
+SIGMAS_STAGE1 = np.array([1.0, 0.99375, 0.9875, 0.98125, 0.975, 0.909375, 0.725, 0.421875, 0.0], np.float32)
+SIGMAS_STAGE2 = np.array([0.909375, 0.725, 0.421875, 0.0], np.float32)
+
+
+def fma_f32(a, b, c) -> np.ndarray:
+    """Correctly rounded f32 a*b + c. The product of two f32 is exact in f64;
+    the f64 sum is taken with round-to-odd (TwoSum error term, then a step to
+    the odd neighbour toward the error), which makes the final rounding to
+    f32 equal the single rounding of the exact value."""
+    a = np.asarray(a, np.float32).astype(np.float64)
+    b = np.asarray(b, np.float32).astype(np.float64)
+    c = np.asarray(c, np.float32).astype(np.float64)
+    p = a * b
+    s = p + c
+    bb = s - p
+    e = (p - (s - bb)) + (c - bb)
+    even = (np.asarray(s, np.float64).view(np.int64) & 1) == 0
+    adj = (e != 0) & even
+    s = np.where(adj, np.nextafter(s, np.where(e > 0, np.inf, -np.inf)), s)
+    return s.astype(np.float32)
+
+
+def sched_lerp(a, b, w, fused: bool = True) -> np.ndarray:
+    """torch.lerp as ltx/scheduler.zig:29-35 computes it: d = b - a; |w| < 0.5
+    -> fma(w, d, a), else fma(-d, 1 - w, b). fused=False evaluates the same
+    forms with two roundings (the reference notes that this differs)."""
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    w = np.broadcast_to(np.asarray(w, np.float32), np.broadcast(a, b).shape)
+    d = (b - a).astype(np.float32)
+    one_m = (np.float32(1.0) - w).astype(np.float32)
+    if fused:
+        lo, hi = fma_f32(w, d, a), fma_f32(-d, one_m, b)
+    else:
+        lo = (w * d).astype(np.float32) + a
+        hi = ((-d) * one_m).astype(np.float32) + b
+    return np.where(np.abs(w) < np.float32(0.5), lo, hi).astype(np.float32)
+
+
+def sched_noise_init(clean, noise, mask_tok, stride: int, noise_scale: float) -> np.ndarray:
+    """noiseInit (ltx/scheduler.zig:41-46); mask_tok [T] per token."""
+    clean = np.asarray(clean, np.float32).reshape(-1)
+    noise = np.asarray(noise, np.float32).reshape(-1)
+    m = np.repeat(np.asarray(mask_tok, np.float32), stride)
+    x = sched_lerp(clean, noise, np.float32(noise_scale))
+    return sched_lerp(clean, x, m)
+
+
+def sched_timesteps(mask, sigma) -> np.ndarray:
+    """ltx/scheduler.zig:49-51."""
+    return (np.asarray(mask, np.float32) * np.float32(sigma)).astype(np.float32)
+
+
+def sched_to_denoised(x, v, ts_tok, stride: int) -> np.ndarray:
+    """ltx/scheduler.zig:57-59."""
+    ts = np.repeat(np.asarray(ts_tok, np.float32), stride)
+    return (np.asarray(x, np.float32).reshape(-1) - (np.asarray(v, np.float32).reshape(-1) * ts)).astype(np.float32)
+
+
+def sched_post_process(den, clean, mask_tok, stride: int) -> np.ndarray:
+    """ltx/scheduler.zig:62-67."""
+    m = np.repeat(np.asarray(mask_tok, np.float32), stride)
+    c = np.asarray(clean, np.float32).reshape(-1)
+    return ((np.asarray(den, np.float32) * m) + (c * (np.float32(1.0) - m))).astype(np.float32)
+
+
+def sched_euler_step(x, post, sigma, sigma_next) -> np.ndarray:
+    """ltx/scheduler.zig:74-80, no snap at sigma_next == 0."""
+    x = np.asarray(x, np.float32).reshape(-1)
+    dt = np.float32(sigma_next) - np.float32(sigma)
+    v = ((x - np.asarray(post, np.float32)) / np.float32(sigma)).astype(np.float32)
+    return (x + (v * dt)).astype(np.float32)
+
+
+def sched_step(x, vel, mask, tidx, clean, sigma, sigma_next):
+    """One march of the loop (ltx/e2e_denoise.zig:321-326) for a latent
+    [T, C] with mask rows `mask` [K] and token rows `tidx` [T]: returns
+    (ts, den, post, next)."""
+    x = np.asarray(x, np.float32)
+    T, Cc = x.shape
+    mask_tok = np.asarray(mask, np.float32)[np.asarray(tidx)]
+    ts = sched_timesteps(mask_tok, sigma)
+    den = sched_to_denoised(x, vel, ts, Cc)
+    post = sched_post_process(den, clean, mask_tok, Cc)
+    nxt = sched_euler_step(x, post, sigma, sigma_next)
+    return ts, den.reshape(T, Cc), post.reshape(T, Cc), nxt.reshape(T, Cc)
+
+
+def denoise(blocks: list, cw: dict, latent, clean, mask, tidx, ctx, cos_thf, sin_thf, sigmas, chunk: int = 16):
+    """The denoising loop (ltx/e2e_denoise.zig:218-336) with K distinct mask
+    rows: per step timesteps -> ts9r / emb / pts2r -> patchify -> blocks (the
+    C oracle, f64 inside, f32 between blocks) -> tail -> the f32 march.
+    Returns the list of (velocity f32 [T, 128], next latent f32 [T, 128])."""
+    lat = np.asarray(latent, np.float32).copy()
+    out = []
+    for s in range(len(sigmas) - 1):
+        sigma, sn = np.float32(sigmas[s]), np.float32(sigmas[s + 1])
+        t = sched_timesteps(mask, sigma)
+        emb = core_emb(cw, t)
+        inp = dict(ctx=ctx, tstab=core_ts9r(cw, t).astype(np.float32), tidx=tidx,
+                   pts2=core_pts2r(cw, sigma).astype(np.float32))
+        x = core_patchify(cw, lat).astype(np.float32)
+        for bt in blocks:
+            inp["x"] = x
+            x = block_forward(bt, inp, cos_thf, sin_thf, chunk=chunk).astype(np.float32)
+        vel = core_tail_from_emb(cw, x, emb[np.asarray(tidx)]).astype(np.float32)
+        _, _, _, lat = sched_step(lat, vel, mask, tidx, clean, sigma, sn)
+        out.append((vel, lat.copy()))
+    return out
