@@ -109,7 +109,7 @@ int ltx_block_forward(ltx_ctx* ctx, const ltx_block_weights* w, const float* x, 
  * valid until the next forward on this context. */
 enum {
     LTX_ST_NORM_MSA,    /* s1NormMsa: modulated norm, operand dtype [T][4096] */
-    LTX_ST_Q1,          /* normed+roped q, head-major [32][T][128] (f32 mode: [T][4096]) */
+    LTX_ST_Q1,          /* normed+roped q times log2(e)/sqrt(128), head-major [32][T][128] (f32 mode: [T][4096], unscaled) */
     LTX_ST_K1,          /* normed+roped k, same layout */
     LTX_ST_V1,          /* v: [32][128][T] (f32 mode: [T][4096]) */
     LTX_ST_GLOG1,       /* gate logits [T][32] f32 */
@@ -136,7 +136,10 @@ int ltx_op_linear_q8(ltx_ctx* ctx, const void* a, const int8_t* q, const void* s
 
 /* Attention with per-(token, head) gate (gate logits glog [Lq][32] f32, or
  * NULL for no gate). F16/BF16: q, k [32][L][128] 16-bit, vt [32][128][Lkv]
- * 16-bit, out [Lq][4096] 16-bit. F32: q, k, v, out [L][4096] f32. */
+ * 16-bit, out [Lq][4096] 16-bit. F32: q, k, v, out [L][4096] f32.
+ * mode | LTX_ATTN_Q_SCALED (16-bit modes): q already holds
+ * q * log2(e) / sqrt(128), as the block's qk-norm writes it (LTX_ST_Q1). */
+#define LTX_ATTN_Q_SCALED 0x100
 int ltx_op_attention(ltx_ctx* ctx, const void* q, const void* k, const void* v, const float* glog, void* out,
                      int lq, int lkv, int mode, void* stream);
 

@@ -161,14 +161,20 @@ static void gate16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
     c->launch(mode == LTX_MODE_BF16 ? "ltx_gate_bf16" : "ltx_gate_f16", (M + 127) / 128, 1, 1, 256, &g, st);
 }
 
+// The attention's exponent scale: softmax scale 1/sqrt(128) times log2(e).
+static const float kAttnC = (float)(1.4426950408889634 / 11.313708498984761);
+
+// oscale multiplies the normed (and roped) rows before the 16-bit rounding:
+// kAttnC for Q, so the attention reads scores in exp2 units, 1 for K.
 static void qknorm16(ltx_ctx* c, int mode, const float* x, int ldx, const void* w, const float* cs, const float* sn,
-                     void* y, int rows, hipStream_t st) {
-    LtxQkNormArgs a{x, (const float*)w, cs, sn, y, rows, ldx};
+                     void* y, int rows, float oscale, hipStream_t st) {
+    LtxQkNormArgs a{x, (const float*)w, cs, sn, y, rows, ldx, oscale};
     c->launch(mode == LTX_MODE_BF16 ? "ltx_qknorm_bf16" : "ltx_qknorm_f16", rows, 1, 1, 256, &a, st);
 }
 
+// q_scaled: Q already carries kAttnC (the block path); else plain Q.
 static void attn16(ltx_ctx* c, int mode, const void* q, const void* k, const void* vt, const float* glog, void* out,
-                   int lq, int lkv, hipStream_t st, const char* label = nullptr) {
+                   int lq, int lkv, bool q_scaled, hipStream_t st, const char* label = nullptr) {
     LtxAttnArgs a;
     a.q = q;
     a.k = k;
@@ -177,13 +183,13 @@ static void attn16(ltx_ctx* c, int mode, const void* q, const void* k, const voi
     a.out = out;
     a.lq = lq;
     a.lkv = lkv;
-    a.scale_log2 = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;
+    a.scale_log2 = q_scaled ? 1.0f : kAttnC;
     int v = c->attn_variant;
     a.q_tiles = (lq + 255) / 256;                    // 256 queries per workgroup
     char name[48];
     if (v == 4) {
         if (lkv % 64 == 0 && lkv >= 128) {  // ping-pong kernel: whole 64-key tiles, at least two
-            std::snprintf(name, sizeof(name), "ltx_attn_%s_pp", msuffix(mode));
+            std::snprintf(name, sizeof(name), "ltx_attn_%s_pp%s", msuffix(mode), q_scaled ? "" : "_uq");
             c->launch(name, a.q_tiles * LTX_H, 1, 1, 512, &a, st, label);
             return;
         }
@@ -318,9 +324,9 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.nsplit = 2 * LTX_D;
     gemm16(c, mode, w->qkv1, b.n_msa, T, LTX_D, LTX_EPI_QKV, g, st, "gemm:qkv1");
     gate16(c, mode, w->g1, b.n_msa, T, (float*)b.glog1, st);
-    qknorm16(c, mode, (const float*)b.qk32, 2 * LTX_D, w->qn1.p, cs, sn, b.qh1, T, st);
-    qknorm16(c, mode, (const float*)b.qk32 + LTX_D, 2 * LTX_D, w->kn1.p, cs, sn, b.kh1, T, st);
-    attn16(c, mode, b.qh1, b.kh1, b.vt1, (const float*)b.glog1, b.o1, T, T, st, "attn:self");
+    qknorm16(c, mode, (const float*)b.qk32, 2 * LTX_D, w->qn1.p, cs, sn, b.qh1, T, kAttnC, st);
+    qknorm16(c, mode, (const float*)b.qk32 + LTX_D, 2 * LTX_D, w->kn1.p, cs, sn, b.kh1, T, 1.0f, st);
+    attn16(c, mode, b.qh1, b.kh1, b.vt1, (const float*)b.glog1, b.o1, T, T, true, st, "attn:self");
     g = LtxGemmArgs{};
     g.out = b.x_sa;
     g.resid = x;
@@ -343,9 +349,9 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.out2 = b.vt2;
     g.nsplit = LTX_D;
     gemm16(c, mode, w->kv2, b.enc, S, LTX_D, LTX_EPI_QKV, g, st, "gemm:kv2");
-    qknorm16(c, mode, (const float*)b.q2_32, LTX_D, w->qn2.p, nullptr, nullptr, b.qh2, T, st);
-    qknorm16(c, mode, (const float*)b.k2_32, LTX_D, w->kn2.p, nullptr, nullptr, b.kh2, S, st);
-    attn16(c, mode, b.qh2, b.kh2, b.vt2, (const float*)b.glog2, b.o2, T, S, st, "attn:cross");
+    qknorm16(c, mode, (const float*)b.q2_32, LTX_D, w->qn2.p, nullptr, nullptr, b.qh2, T, kAttnC, st);
+    qknorm16(c, mode, (const float*)b.k2_32, LTX_D, w->kn2.p, nullptr, nullptr, b.kh2, S, 1.0f, st);
+    attn16(c, mode, b.qh2, b.kh2, b.vt2, (const float*)b.glog2, b.o2, T, S, true, st, "attn:cross");
     g = LtxGemmArgs{};
     g.out = b.x_ca;
     g.resid = (const float*)b.x_sa;
@@ -447,12 +453,15 @@ int ltx_op_attention(ltx_ctx* c, const void* q, const void* k, const void* v, co
     LTX_GUARD(c, {
         if (!c) throw ltx::Error("NULL context");
         if (lq <= 0 || lkv <= 0) throw ltx::Error("bad attention lengths");
+        const bool q_scaled = (mode & LTX_ATTN_Q_SCALED) != 0;
+        mode &= ~LTX_ATTN_Q_SCALED;
+        if (q_scaled && mode == LTX_MODE_F32) throw ltx::Error("LTX_ATTN_Q_SCALED applies to the 16-bit modes");
         HIPC(hipSetDevice(c->device));
         if (mode == LTX_MODE_F32)
             ltx::attn32(c, (const float*)q, (const float*)k, (const float*)v, glog, (float*)out, lq, lkv,
                         (hipStream_t)stream);
         else
-            ltx::attn16(c, mode, q, k, v, glog, out, lq, lkv, (hipStream_t)stream);
+            ltx::attn16(c, mode, q, k, v, glog, out, lq, lkv, q_scaled, (hipStream_t)stream);
     })
 }
 

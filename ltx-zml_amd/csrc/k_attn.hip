@@ -687,7 +687,9 @@ __device__ __forceinline__ uint8_t* app_v() {
     return S == 0 ? app_v0 : S == 1 ? app_v1 : app_v2;
 }
 
-template <typename T>
+// PS: Q arrives multiplied by the exponent scale C = log2(e)/sqrt(128) (the
+// block's qk-norm kernel writes it so), so a score is already in exp2 units.
+template <typename T, bool PS>
 struct AttnPP {
     typedef typename Op<T>::v8 v8;
     const LtxAttnArgs& a;
@@ -700,6 +702,7 @@ struct AttnPP {
     f32x16 o[4];
     f32x16 s[2];
     v8 pf[4];
+    f32x16 sb;  // -m in every element: the S MFMAs start from it, so s holds s - m
     float m, l, C;
     int nt, g;
 
@@ -735,8 +738,8 @@ struct AttnPP {
         }
         if (ds) {
             const uint8_t* sk = app_k<KS>();
-            s[0] = f32x16{0};
-            s[1] = f32x16{0};
+            s[0] = sb;
+            s[1] = sb;
 #pragma unroll
             for (int c = 0; c < 8; c++)
 #pragma unroll
@@ -754,22 +757,29 @@ struct AttnPP {
         }
     }
 
-    // P^T operands and their row sum for the running max m (exp2 of
-    // s C - m C, the 1/sqrt(128) scale folded into C)
-    __device__ __forceinline__ float exps() {
-        const float mc = m * C;
+    // P^T operands and their row sum. s holds score - m (the MFMAs start from
+    // sb = -m), so the weight is exp2(s) with Q pre-scaled (PS), else
+    // exp2(s C); ADJ subtracts a further max shift delta. The row sum adds
+    // exactly the rounded 16-bit weights that feed the MFMA, on the VALU.
+    template <bool ADJ>
+    __device__ __forceinline__ float exps(float delta) {
         float ps = 0.f;
 #pragma unroll
         for (int kc = 0; kc < 4; kc++) {
             float p[8];
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-                p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kc >> 1][8 * (kc & 1) + e], C, -mc));
-            const u32x4 pk4 = {Op<T>::cvt2(p[0], p[1]), Op<T>::cvt2(p[2], p[3]), Op<T>::cvt2(p[4], p[5]),
-                               Op<T>::cvt2(p[6], p[7])};
-#pragma unroll
-            for (int e = 0; e < 4; e++) ps = Op<T>::sum2(pk4[e], ps);
-            pf[kc] = __builtin_bit_cast(v8, pk4);
+            for (int e = 0; e < 8; e++) {
+                float x = s[kc >> 1][8 * (kc & 1) + e];
+                if (ADJ) x -= delta;
+                p[e] = __builtin_amdgcn_exp2f(PS ? x : x * C);
+            }
+            const uint32_t w0 = Op<T>::cvt2(p[0], p[1]), w1 = Op<T>::cvt2(p[2], p[3]),
+                           w2 = Op<T>::cvt2(p[4], p[5]), w3 = Op<T>::cvt2(p[6], p[7]);
+            ps = Op<T>::sum2(w0, ps);
+            ps = Op<T>::sum2(w1, ps);
+            ps = Op<T>::sum2(w2, ps);
+            ps = Op<T>::sum2(w3, ps);
+            pf[kc] = __builtin_bit_cast(v8, (u32x4){w0, w1, w2, w3});
         }
         return ps;
     }
@@ -779,23 +789,24 @@ struct AttnPP {
     // weights exceeds 2^8 (a weight above 2^8, or an f16 overflow, which sums
     // to inf) is the tile max taken, the max moved, the output and row sum
     // rescaled (after PV(t-1), before PV(t)) and the weights formed again.
-    // The first tile always takes that path (m starts at -FLT_MAX).
-    __device__ __forceinline__ void softmax() {
-        float ps = exps();
-        if (__builtin_amdgcn_ballot_w64(!(ps <= 256.0f)) != 0) {
+    // The first tile always takes that path and sets m to its max.
+    __device__ __forceinline__ void softmax(bool first) {
+        float ps = exps<false>(0.f);
+        if (first || __builtin_amdgcn_ballot_w64(!(ps <= 256.0f)) != 0) {
             float mx = s[0][0];
 #pragma unroll
             for (int r = 1; r < 16; r++) mx = fmaxf(mx, s[0][r]);
 #pragma unroll
             for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[1][r]);
-            mx = asp_xhalf_max(mx);
-            const float mn = fmaxf(m, mx);
-            const float corr = __builtin_amdgcn_exp2f((m - mn) * C);
-            m = mn;
+            mx = asp_xhalf_max(mx);  // tile max relative to m
+            const float delta = first ? mx : fmaxf(mx, 0.f);
+            const float corr = first ? 0.f : __builtin_amdgcn_exp2f(PS ? -delta : -delta * C);
+            m += delta;
             l *= corr;
 #pragma unroll
             for (int db = 0; db < 4; db++) o[db] *= corr;
-            ps = exps();
+            sb = f32x16{0} - m;
+            ps = exps<true>(delta);
         }
         l += ps;
     }
@@ -821,12 +832,13 @@ struct AttnPP {
         if (dk) dma_k<(T3 + 2) % 3>(t + 2);
         if (dv) dma_v<(T3 + 1) % 3>(t + 1);
         __builtin_amdgcn_sched_barrier(0);
-        softmax();
-        // the P^T operands and row sum must exist before the phase ends (no
-        // pass may sink them into the next MFMA phase)
+        softmax(!FULL && t == 0);
+        // the P^T operands, row sum and bias must exist before the phase ends
+        // (no pass may sink them into the next MFMA phase)
 #pragma unroll
         for (int kc = 0; kc < 4; kc++) asm volatile("" ::"v"(__builtin_bit_cast(u32x4, pf[kc])));
         asm volatile("" ::"v"(l), "v"(m));
+        asm volatile("" ::"v"(sb));
         __builtin_amdgcn_sched_barrier(0);
         if (g == 0) {
             if (dk && dv)
@@ -882,7 +894,8 @@ struct AttnPP {
         }
 #pragma unroll
         for (int db = 0; db < 4; db++) o[db] = f32x16{0};
-        m = -3.402823466e38f;
+        m = 0.f;
+        sb = f32x16{0};
         l = 0.f;
         // prologue: K(0), K(1), V(0); MFMA phase 0 needs K(0)
         dma_k<0>(0);
@@ -942,11 +955,20 @@ struct AttnPP {
     }
 };
 
+// _pp: Q pre-scaled by scale_log2 (the block's layout); _pp_uq: plain Q.
 extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_f16_pp(const LtxAttnArgs a) {
-    AttnPP<_Float16> k(a);
+    AttnPP<_Float16, true> k(a);
     k.run();
 }
 extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_bf16_pp(const LtxAttnArgs a) {
-    AttnPP<__bf16> k(a);
+    AttnPP<__bf16, true> k(a);
+    k.run();
+}
+extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_f16_pp_uq(const LtxAttnArgs a) {
+    AttnPP<_Float16, false> k(a);
+    k.run();
+}
+extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_bf16_pp_uq(const LtxAttnArgs a) {
+    AttnPP<__bf16, false> k(a);
     k.run();
 }

@@ -122,6 +122,11 @@ __device__ void qknorm_body(const LtxQkNormArgs& a) {
             hi[j] = x1 * c + x0 * s;
         }
     }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        lo[j] *= a.oscale;
+        hi[j] *= a.oscale;
+    }
     uint16_t* y = (uint16_t*)a.y + ((size_t)h * a.rows + row) * LTX_HD;
     u32x4 plo = {pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3]), pack2<T>(lo[4], lo[5]), pack2<T>(lo[6], lo[7])};
     u32x4 phi = {pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3]), pack2<T>(hi[4], hi[5]), pack2<T>(hi[6], hi[7])};

@@ -85,6 +85,7 @@ typedef struct {
     void* y;            // [H][rows][HD]
     int rows;
     int ldx;
+    float oscale;       // applied before the 16-bit rounding (1, or the attention's exponent scale for Q)
 } LtxQkNormArgs;
 
 // Blockwise online-softmax attention with per-(token, head) gate.

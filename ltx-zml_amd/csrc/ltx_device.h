@@ -39,10 +39,16 @@ struct Op<_Float16> {
     static __device__ __forceinline__ uint32_t cvt2(float a, float b) {
         return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
     }
-    // acc + lo + hi of a packed pair (v_dot2c_f32_f16 with (1, 1))
+    // acc + lo + hi of a packed pair, each half widened exactly (two
+    // v_fma_mix_f32 with 1.0). The dot2 forms would do this in one
+    // instruction, but they issue to the matrix pipeline and wait behind
+    // another wave's MFMAs.
     static __device__ __forceinline__ float sum2(uint32_t p, float acc) {
-        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p), (f16x2){(_Float16)1.0f, (_Float16)1.0f}, acc,
-                                      false);
+        asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+            : "+v"(acc)
+            : "v"(p));
+        return acc;
     }
 };
 
@@ -62,9 +68,10 @@ struct Op<__bf16> {
     static __device__ __forceinline__ uint32_t cvt2(float a, float b) {
         return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
     }
+    // acc + lo + hi of a packed pair, widened exactly on the VALU (see the
+    // f16 form)
     static __device__ __forceinline__ float sum2(uint32_t p, float acc) {
-        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p), (bf16x2){(__bf16)1.0f, (__bf16)1.0f},
-                                               acc, false);
+        return (acc + __builtin_bit_cast(float, p << 16)) + __builtin_bit_cast(float, p & 0xffff0000u);
     }
 };
 

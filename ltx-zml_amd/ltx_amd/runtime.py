@@ -17,6 +17,8 @@ PKG_DIR = pathlib.Path(__file__).resolve().parent.parent
 LIB_PATH = PKG_DIR / "libltx_amd.so"
 
 MODE_F16, MODE_BF16, MODE_F32 = 0, 1, 2
+ATTN_Q_SCALED = 0x100  # ltx_op_attention mode flag
+ATTN_C = float(np.float32(1.4426950408889634 / 11.313708498984761))  # log2(e) / sqrt(128)
 MODES = {"f16": MODE_F16, "bf16": MODE_BF16, "f32": MODE_F32}
 STAGES = ["norm_msa", "q1", "k1", "v1", "glog1", "attn1", "x_sa", "attn_in", "attn2", "x_ca", "ff_in", "ff_h"]
 
@@ -239,10 +241,12 @@ class Context:
                                            mode, st), "ltx_op_linear_q8")
         return y
 
-    def attention(self, q, k, v, glog, out, lq, lkv, mode=MODE_F16, stream=None):
+    def attention(self, q, k, v, glog, out, lq, lkv, mode=MODE_F16, stream=None, q_scaled=False):
+        """q_scaled: q already holds q * log2(e) / sqrt(128) (LTX_ATTN_Q_SCALED)."""
         st = stream.cuda_stream if stream is not None else _current_stream()
+        m = mode | (ATTN_Q_SCALED if q_scaled else 0)
         self._check(lib().ltx_op_attention(self.handle, _ptr(q), _ptr(k), _ptr(v), _ptr(glog), _ptr(out), lq, lkv,
-                                           mode, st), "ltx_op_attention")
+                                           m, st), "ltx_op_attention")
         return out
 
     def dequant(self, q, s, out32, out16, mode=MODE_F16, stream=None):

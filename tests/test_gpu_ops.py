@@ -173,22 +173,26 @@ def _heads(x, L):  # [L, D] -> [H, L, 128]
                                           (64, 77, True),
                                           # pipelined kernel (whole 32-key tiles, >= 4): shortest loop, tails
                                           (100, 128, True), (300, 160, True), (256, 480, False)])
-def test_attention(ctx, mode, lq, lkv, gated):
-    say(f"attention mode={mode} lq={lq} lkv={lkv} gated={gated}")
+@pytest.mark.parametrize("q_scaled", [False, True])
+def test_attention(ctx, mode, lq, lkv, gated, q_scaled):
+    """q_scaled: q arrives multiplied by log2(e)/sqrt(128), as the block's
+    qk-norm writes it; the oracle then takes that q divided back (exactly)."""
+    say(f"attention mode={mode} lq={lq} lkv={lkv} gated={gated} q_scaled={q_scaled}")
     m, dt = MODES[mode]
     rng = np.random.default_rng(lq * 7 + lkv)
     q = rng.standard_normal((lq, 4096)).astype(np.float32)
     k = rng.standard_normal((lkv, 4096)).astype(np.float32)
     v = rng.standard_normal((lkv, 4096)).astype(np.float32)
     glog = rng.standard_normal((lq, 32)).astype(np.float32) if gated else None
-    dq = to16(_heads(q, lq), dt).cuda()
+    cq = rt.ATTN_C if q_scaled else 1.0
+    dq = to16(_heads(q * np.float32(cq), lq), dt).cuda()
     dk = to16(_heads(k, lkv), dt).cuda()
     dv = to16(np.ascontiguousarray(v.reshape(lkv, 32, 128).transpose(1, 2, 0)), dt).cuda()  # [H][128][L]
     dg = torch.from_numpy(glog).cuda() if gated else None
     out = torch.empty((lq, 4096), dtype=dt, device="cuda")
-    ctx.attention(dq, dk, dv, dg, out, lq, lkv, mode=m)
+    ctx.attention(dq, dk, dv, dg, out, lq, lkv, mode=m, q_scaled=q_scaled)
     torch.cuda.synchronize()
-    q64 = f64(dq).transpose(1, 0, 2).reshape(lq, 4096)
+    q64 = f64(dq).transpose(1, 0, 2).reshape(lq, 4096) / cq
     k64 = f64(dk).transpose(1, 0, 2).reshape(lkv, 4096)
     v64 = f64(dv).transpose(2, 0, 1).reshape(lkv, 4096)
     want = oracle.sdpa(q64, k64, v64, chunk=0)
@@ -214,21 +218,23 @@ def test_attention_f32_mode(ctx):
     assert oracle.rel_rms(f64(out), want) <= 1e-5
 
 
-@pytest.mark.parametrize("lkv,dom", [(96, 37), (160, 130)])
-def test_attention_special_cases(ctx, lkv, dom):
+@pytest.mark.parametrize("lkv,dom", [(96, 37), (160, 130), (256, 200)])
+@pytest.mark.parametrize("q_scaled", [False, True])
+def test_attention_special_cases(ctx, lkv, dom, q_scaled):
     """Identical keys -> mean of V; one dominant key -> that V row (placed
     past the first tiles, so the running max must move and rescale O)."""
-    say(f"attention special cases f16 lkv={lkv} dominant key={dom}")
+    say(f"attention special cases f16 lkv={lkv} dominant key={dom} q_scaled={q_scaled}")
+    cq = np.float32(rt.ATTN_C if q_scaled else 1.0)
     rng = np.random.default_rng(12)
     lq = 64
     q = rng.standard_normal((lq, 4096)).astype(np.float32)
     k = np.tile(rng.standard_normal((1, 4096)).astype(np.float32), (lkv, 1))
     v = rng.standard_normal((lkv, 4096)).astype(np.float32)
     dt = torch.float16
-    args = [to16(_heads(q, lq), dt).cuda(), to16(_heads(k, lkv), dt).cuda(),
+    args = [to16(_heads(q * cq, lq), dt).cuda(), to16(_heads(k, lkv), dt).cuda(),
             to16(np.ascontiguousarray(v.reshape(lkv, 32, 128).transpose(1, 2, 0)), dt).cuda()]
     out = torch.empty((lq, 4096), dtype=dt, device="cuda")
-    ctx.attention(*args, None, out, lq, lkv, mode=rt.MODE_F16)
+    ctx.attention(*args, None, out, lq, lkv, mode=rt.MODE_F16, q_scaled=q_scaled)
     torch.cuda.synchronize()
     vm = f64(args[2]).transpose(2, 0, 1).reshape(lkv, 4096).mean(0)
     assert np.abs(f64(out) - vm[None, :]).max() < 2e-3
@@ -236,8 +242,8 @@ def test_attention_special_cases(ctx, lkv, dom):
     k2 = rng.standard_normal((lkv, 4096)).astype(np.float32) * 0.01
     qq = np.tile(rng.standard_normal((1, 4096)).astype(np.float32), (lq, 1))
     k2[dom] = qq[0] * 4.0
-    args2 = [to16(_heads(qq, lq), dt).cuda(), to16(_heads(k2, lkv), dt).cuda(), args[2]]
-    ctx.attention(*args2, None, out, lq, lkv, mode=rt.MODE_F16)
+    args2 = [to16(_heads(qq * cq, lq), dt).cuda(), to16(_heads(k2, lkv), dt).cuda(), args[2]]
+    ctx.attention(*args2, None, out, lq, lkv, mode=rt.MODE_F16, q_scaled=q_scaled)
     torch.cuda.synchronize()
     vd = f64(args[2]).transpose(2, 0, 1).reshape(lkv, 4096)[dom]
     assert np.abs(f64(out) - vd[None, :]).max() < 5e-3
