@@ -88,12 +88,34 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
     const bool f32out = EPI != LTX_EPI_STORE || a.out_f32;
 #pragma unroll
     for (int i = 0; i < NI; i++) {
+        const int mb = mw + 32 * i;
+        // gated residual: this block's residual rows and gate rows are loaded
+        // before anything is stored (the stores could alias them for the
+        // compiler, which would otherwise wait out one load round trip per
+        // row group)
+        constexpr int RLPR = WN / 4, RRPP = 64 / RLPR, RNP = 32 / RRPP;
+        f32x4 rs[EPI == LTX_EPI_RESID_GATE ? RNP : 1], gt[EPI == LTX_EPI_RESID_GATE ? RNP : 1];
+        if (EPI == LTX_EPI_RESID_GATE) {
+            const int c4 = 4 * (lane % RLPR), r0 = lane / RLPR;
+            const int n = nw + c4;
+            int tix[RNP];
+#pragma unroll
+            for (int p = 0; p < RNP; p++) {
+                const int m = min(mb + r0 + RRPP * p, a.M - 1);
+                tix[p] = a.ada.tidx[m];
+            }
+#pragma unroll
+            for (int p = 0; p < RNP; p++) {
+                const int m = min(mb + r0 + RRPP * p, a.M - 1);
+                rs[p] = *(const f32x4*)(a.resid + (size_t)m * a.ldo + n);
+                gt[p] = *(const f32x4*)(a.ada.tstab + ((size_t)tix[p] * 9 + a.igate) * LTX_D + n);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < NJ; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++)
                 patch[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * LD + 32 * j + (lane & 31)] = acc[i][j][r];
-        const int mb = mw + 32 * i;
         if (vt) {
             // V^T [c][m]: 4 lanes cover one column's 32 rows (64 contiguous bytes)
             const int rg = lane & 3;
@@ -132,11 +154,8 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
                     if (a.gelu) v = f32x4{gelu_tanh(v[0]), gelu_tanh(v[1]), gelu_tanh(v[2]), gelu_tanh(v[3])};
                     *(f32x4*)((float*)a.out + (size_t)m * a.ldo + n) = v;
                 } else if (EPI == LTX_EPI_RESID_GATE) {
-                    const f32x4 gt =
-                        *(const f32x4*)(a.ada.tstab + ((size_t)a.ada.tidx[m] * 9 + a.igate) * LTX_D + n);
                     const size_t o = (size_t)m * a.ldo + n;
-                    const f32x4 rs = *(const f32x4*)(a.resid + o);
-                    *(f32x4*)((float*)a.out + o) = rs + v * (gt + gs);
+                    *(f32x4*)((float*)a.out + o) = rs[p] + v * (gt[p] + gs);
                 } else {  // q | k part of the fused QKV projection
                     *(f32x4*)((float*)a.out + (size_t)m * a.nsplit + n) = v;
                 }
