@@ -157,6 +157,9 @@ struct Q8Gemm {
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
+            // the wave in its MFMA phase takes issue priority over the other
+            // wave of its SIMD (without it the lower-numbered waves win)
+            __builtin_amdgcn_s_setprio(1);
         }
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -177,6 +180,7 @@ struct Q8Gemm {
                                                                         acc[i][j], 0, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
+        if (PP) __builtin_amdgcn_s_setprio(0);
         if (!PP || g == 0) wait_dma(more2);
         __builtin_amdgcn_s_waitcnt(Q8_WAIT_LGKM0);
         __builtin_amdgcn_s_barrier();

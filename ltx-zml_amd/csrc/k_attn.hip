@@ -823,8 +823,12 @@ struct AttnPP {
     // FULL: 1 <= t and t + 2 < nt, every operation present.
     template <int T3, bool FULL>
     __device__ __forceinline__ void step(int t) {
+        // the wave in its MFMA phase takes issue priority over the other wave
+        // of its SIMD (without it the lower-numbered waves win either way)
+        __builtin_amdgcn_s_setprio(1);
         mfma_phase<T3, (T3 + 2) % 3>(FULL || t < nt, FULL || t >= 1);
         __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
         if (g == 1) __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(0));
         barrier();
         if (!FULL && t >= nt) return;
