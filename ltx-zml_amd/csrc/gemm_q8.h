@@ -15,10 +15,11 @@
 // every wave dequantises the fragments it reads (half the LDS bytes of an f16
 // tile, no second LDS pass).
 //
-// Dequantisation is exact: for u = q + 128 (the byte read as unsigned), the
-// f16 with bits 0x6400 | u is 1024 + u; subtracting 1152 gives q exactly and
-// one f16 multiply by the f16 scale rounds q * s once to nearest even — the
-// operand RNE16(q * s) that the register-staged kernels also feed the MFMA.
+// Dequantisation is exact: the weight bytes are stored as u = q + 128 (q XOR
+// 0x80, done once at upload), the f16 with bits 0x6400 | u is 1024 + u;
+// subtracting 1152 gives q exactly and one f16 multiply by the f16 scale
+// rounds q * s once to nearest even — the operand RNE16(q * s) that the
+// register-staged kernels also feed the MFMA.
 //
 // LDS layout: A rows of 128 B (8 chunks of 8 k), chunk c of row r stored in
 // slot c ^ ((r >> 1) & 7) (16 consecutive rows, one ds_read_b128 lane group,
@@ -63,14 +64,14 @@ __device__ __forceinline__ uint8_t* q8_stage_b() {
     return S == 0 ? q8_sb0 : S == 1 ? q8_sb1 : q8_sb2;
 }
 
-// 8 int8 weights (two dwords of an LDS chunk) -> one f16x8 operand, times
-// the scale pair s2.
+// 8 weights (two dwords of an LDS chunk, bytes q + 128) -> one f16x8
+// operand, times the scale pair s2.
 __device__ __forceinline__ f16x8 q8_dequant8(uint32_t w0, uint32_t w1, f16x2 s2) {
     const f16x2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
     uint32_t o[4];
 #pragma unroll
     for (int d = 0; d < 2; d++) {
-        const uint32_t x = (d ? w1 : w0) ^ 0x80808080u;
+        const uint32_t x = d ? w1 : w0;
         const f16x2 p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u));
         const f16x2 p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u));
         o[2 * d] = __builtin_bit_cast(uint32_t, (p0 - off) * s2);

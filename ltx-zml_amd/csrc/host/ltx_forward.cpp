@@ -125,6 +125,7 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
     if (p.q8) {
         g.b = p.q.p;
         g.scales = p.s.p;
+        g.qxor = p.qflip ? 0u : 0x80808080u;
         bk = p.scale_f16 ? "i8f16" : "i8f32";
     } else {
         g.b = mode == LTX_MODE_BF16 ? p.w_bf16.p : p.w_f16.p;
@@ -139,7 +140,7 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
     // LDS-DMA int8 kernel: f16 operands, f16 scales, K a multiple of 128, and
     // byte offsets of A and W within 31 bits (32-bit buffer offsets)
     auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
-    if (mode == LTX_MODE_F16 && p.q8 && p.scale_f16 && p.s2.p && c->gemm_q8 != 0 && p.K % 128 == 0 &&
+    if (mode == LTX_MODE_F16 && p.q8 && p.qflip && p.scale_f16 && p.s2.p && c->gemm_q8 != 0 && p.K % 128 == 0 &&
         (uint64_t)M * lda * 2 < (1ull << 31) && (uint64_t)p.N * p.K < (1ull << 31) && g.ldo % 8 == 0 &&
         al16(g.out) && al16(g.out2) && al16(g.resid) && al16(g.bias) && al16(g.ada.tstab) && al16(g.ada.sst)) {
         // (its epilogue moves 16-byte vectors: outputs, residual and bias 16-byte aligned)
@@ -217,6 +218,7 @@ static void gemm32(ltx_ctx* c, const LtxProj& p, int r0, int N, const float* A, 
     const size_t G = p.K / LTX_GROUP;
     if (p.q8) {
         g.bkind = p.scale_f16 ? 1 : 0;
+        g.qxor = p.qflip ? 0u : 0x80808080u;
         g.b = (const int8_t*)p.q.p + (size_t)r0 * p.K;
         g.scales = (const char*)p.s.p + (size_t)r0 * G * (p.scale_f16 ? 2 : 4);
     } else {
@@ -432,6 +434,13 @@ int ltx_op_linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* sca
                     LtxPairArgs pa{(const uint16_t*)scales, (uint32_t*)c->op_pairs.p, N, K / LTX_GROUP};
                     c->launch("ltx_scale_pairs", (unsigned)((n2 + 255) / 256), 1, 1, 256, &pa, (hipStream_t)stream);
                     p.s2.p = c->op_pairs.p;
+                    // and its weights as the bytes q + 128
+                    const size_t nq = (size_t)N * K / 4;
+                    if (c->op_q.bytes < nq * 4) c->op_q.alloc(nq * 4);
+                    LtxFlipArgs fa{(const uint32_t*)q, (uint32_t*)c->op_q.p, nq};
+                    c->launch("ltx_q8_flip", (unsigned)((nq + 255) / 256), 1, 1, 256, &fa, (hipStream_t)stream);
+                    p.q.p = c->op_q.p;
+                    p.qflip = true;
                 }
                 LtxGemmArgs g{};
                 g.out = y;

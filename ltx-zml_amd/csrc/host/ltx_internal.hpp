@@ -46,6 +46,7 @@ struct ProfRec {
 struct LtxProj {
     int N = 0, K = 0;
     bool q8 = false;          // int8 + scales available
+    bool qflip = false;       // q holds the bytes q + 128 (q XOR 0x80)
     int scale_f16 = 0;
     ltx::DevBuf q;            // int8 [N][K]
     ltx::DevBuf s;            // [N][K/128] f32 or f16
@@ -85,6 +86,7 @@ struct ltx_ctx {
     // workspace
     ltx::DevBuf ws;
     ltx::DevBuf op_pairs;  // scale pairs of the last ltx_op_linear_q8 call (f16 scales)
+    ltx::DevBuf op_q;      // its weights as bytes q + 128
     ltx::DevBuf core_ws;   // conditioning MLP rows
     ltx::DevBuf tail_ws;   // normed rows of ltx_core_tail
     ltx::DevBuf dn_ws;     // the denoising loop's activations

@@ -176,6 +176,7 @@ void ltx_destroy(ltx_ctx* c) {
     for (auto e : c->ev_pool) (void)hipEventDestroy(e);
     c->ws.free_();
     c->op_pairs.free_();
+    c->op_q.free_();
     c->core_ws.free_();
     c->tail_ws.free_();
     c->dn_ws.free_();

@@ -82,16 +82,25 @@ static void build_proj(LtxProj& p, const void* const* base, const int8_t* const*
     p.scale_f16 = sf16;
     const size_t G = K / LTX_GROUP;
     if (all_q8) {
-        std::vector<int8_t> q((size_t)p.N * K);
+        // weights stored as the bytes q + 128 (XOR 0x80): the LDS-DMA GEMM
+        // then needs no per-byte flip (K is a multiple of 128, so of 8)
+        std::vector<uint64_t> q((size_t)p.N * K / 8);
         std::vector<char> s((size_t)p.N * G * (sf16 ? 2 : 4));
         size_t r = 0;
         for (size_t j = 0; j < ids.size(); j++) {
             int qi = ids[j];
-            std::memcpy(q.data() + r * K, q8[qi], (size_t)Ns[j] * K);
+            const size_t nw = (size_t)Ns[j] * K / 8;
+            uint64_t* dst = q.data() + r * K / 8;
+            for (size_t i = 0; i < nw; i++) {
+                uint64_t v;
+                std::memcpy(&v, (const char*)q8[qi] + 8 * i, 8);
+                dst[i] = v ^ 0x8080808080808080ull;
+            }
             std::memcpy(s.data() + r * G * (sf16 ? 2 : 4), q8s[qi], (size_t)Ns[j] * G * (sf16 ? 2 : 4));
             r += Ns[j];
         }
-        h2d(p.q, q.data(), q.size());
+        h2d(p.q, q.data(), q.size() * 8);
+        p.qflip = true;
         h2d(p.s, s.data(), s.size());
         if (sf16) {  // f16 scales also as pairs (s | s << 16), u32 [G][N], for the LDS-DMA kernels
             const uint16_t* s16 = (const uint16_t*)s.data();

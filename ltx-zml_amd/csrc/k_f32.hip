@@ -26,7 +26,7 @@ extern "C" __global__ void __launch_bounds__(256) ltx_gemm_f32(const LtxGemm32Ar
             } else {
                 size_t si = (size_t)n * G + (k0 + k) / LTX_GROUP;
                 float s = a.bkind == 1 ? f16_bits_to_f32(((const uint16_t*)a.scales)[si]) : ((const float*)a.scales)[si];
-                bv = (float)((const int8_t*)a.b)[bi] * s;
+                bv = (float)((int)(((const uint8_t*)a.b)[bi] ^ (a.qxor & 0xffu)) - 128) * s;
             }
             sB[k][r] = bv;
         }

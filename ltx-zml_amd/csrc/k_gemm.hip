@@ -50,7 +50,7 @@ struct Stage {
 #pragma unroll
             for (int i = 0; i < NB8; i++) {
                 int r = n0 + (tid >> 2) + (NT / 4) * i;
-                rb[i] = *(const u32x4*)(B + (size_t)r * a.K + k0 + 16 * cb);
+                rb[i] = *(const u32x4*)(B + (size_t)r * a.K + k0 + 16 * cb) ^ a.qxor;  // -> bytes q + 128
                 size_t si = (size_t)r * G + (k0 + 16 * cb) / LTX_GROUP;
                 sc[i] = BKIND == LTX_B_I8_F16S ? f16_bits_to_f32(((const uint16_t*)a.scales)[si])
                                               : ((const float*)a.scales)[si];
@@ -73,7 +73,7 @@ struct Stage {
                 uint32_t o[8];
 #pragma unroll
                 for (int d = 0; d < 4; d++) {
-                    uint32_t w = rb[i][d] ^ 0x80808080u;
+                    const uint32_t w = rb[i][d];  // bytes q + 128
                     o[2 * d] = deq_pack2<T>((float)(w & 0xffu), (float)((w >> 8) & 0xffu), s, nb);
                     o[2 * d + 1] = deq_pack2<T>((float)((w >> 16) & 0xffu), (float)(w >> 24), s, nb);
                 }

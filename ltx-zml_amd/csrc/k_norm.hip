@@ -202,6 +202,11 @@ extern "C" __global__ void __launch_bounds__(256) ltx_dequant_f16(const LtxDequa
 extern "C" __global__ void __launch_bounds__(256) ltx_dequant_bf16(const LtxDequantArgs a) { dequant_body<__bf16>(a); }
 
 // Scale pairs for the LDS-DMA int8 GEMM: out[g][n] = s[n][g] in both halves.
+extern "C" __global__ void __launch_bounds__(256) ltx_q8_flip(const LtxFlipArgs a) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < a.n) a.out[i] = a.in[i] ^ 0x80808080u;
+}
+
 extern "C" __global__ void __launch_bounds__(256) ltx_scale_pairs(const LtxPairArgs a) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= a.N * a.G) return;

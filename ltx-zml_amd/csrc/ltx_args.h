@@ -73,6 +73,8 @@ typedef struct {
     int gelu;             // STORE: apply GELU-tanh
     int out_f32;          // STORE: 1 = f32 output, 0 = 16-bit output
     int tiles_m, tiles_n; // grid geometry (filled by host)
+    uint32_t qxor;        // int8 kinds: XOR taking each weight byte to q + 128 (0x80808080 for plain int8,
+                          // 0 for bytes stored as q + 128); the LDS-DMA kernels take the latter only
 } LtxGemmArgs;
 
 // Full-row qk RMSNorm (weighted, over all 4096 channels) + optional split-half
@@ -122,6 +124,13 @@ typedef struct {
     int scale_f16;
 } LtxDequantArgs;
 
+// int8 weights -> bytes q + 128 (XOR 0x80 per byte), n words of 4 bytes.
+typedef struct {
+    const uint32_t* in;
+    uint32_t* out;
+    size_t n;
+} LtxFlipArgs;
+
 // f16 scales [N][G] -> scale pairs u32 [G][N] (s | s << 16) for the LDS-DMA
 // int8 GEMM.
 typedef struct {
@@ -144,6 +153,7 @@ typedef struct {
     int epi;            // LTX_EPI_STORE / RESID_GATE
     int gelu;
     int igate;
+    uint32_t qxor;      // int8 kinds: as LtxGemmArgs.qxor
 } LtxGemm32Args;
 
 typedef struct {
