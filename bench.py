@@ -31,7 +31,7 @@ PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
 # HBM bytes per self-attention launch from rocprofv3 FETCH_SIZE (x2.0, the
 # factor a 1 GiB copy calibrates) + WRITE_SIZE (x1.0), for the kernel as
 # built at that measurement (profiles/attn_self_t28672_f16_hbm_bytes.md).
-ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.467e9}
+ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.469e9}
 
 
 def flops(T: int, S: int) -> dict:
@@ -91,6 +91,71 @@ def cpu_baseline(T: int, S: int, threads: int) -> dict:
     }
 
 
+def denoise_bench(args) -> int:
+    """Stage-1 denoising loop (ltx/e2e_denoise.zig:218-336): 8 Euler steps,
+    each conditioning -> patchify -> every resident block -> tail -> march,
+    all on the GPU (ltx_denoise). The blocks are copies of one seeded int8
+    block (resident weights, the same arithmetic per block)."""
+    import numpy as np
+    import torch
+
+    from ltx_amd import conditioning
+    from ltx_amd import runtime as rt
+    from ltx_amd import synth
+
+    T, S, nb = args.tokens, args.text, args.denoise
+    t0 = time.time()
+    bt = synth.make_block(0, seed=1, dist="t3", classes=("qkv", "ff", "out"), scale_dtype="F16")
+    ctx = rt.Context(0)
+    blocks = [ctx.upload(bt) for _ in range(nb)]
+    del bt
+    cw = ctx.upload_core(conditioning.make_core(7))
+    g = np.random.default_rng(3)
+    clean = g.standard_normal((T, 128)).astype(np.float32)
+    noise = g.standard_normal((T, 128)).astype(np.float32)
+    mask, tidx = conditioning.mask_rows(T)
+    ctx_tok = synth.rng(2, "ctx").standard_normal((S, D), dtype=np.float32)
+    cos, sin = rt.rope_tables(synth.grid_for_tokens(T))
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    dclean, dnoise, dmask, dtidx, dctx, dcos, dsin = (dev(a) for a in (clean, noise, mask, tidx, ctx_tok, cos, sin))
+    lat = torch.empty((T, 128), dtype=torch.float32, device="cuda")
+    sig = rt.sched_sigmas(1)
+    mode = rt.MODES[args.mode]
+    log(f"bench: {nb} blocks resident, inputs ready in {time.time() - t0:.1f}s")
+    # warm-up: one step
+    ctx.noise_init(dclean, dnoise, dmask, dtidx, float(sig[0]), lat)
+    ctx.denoise(blocks, cw, lat, dclean, dmask, dtidx, dctx, dcos, dsin, sig[:2], mode=mode)
+    torch.cuda.synchronize()
+    ctx.noise_init(dclean, dnoise, dmask, dtidx, float(sig[0]), lat)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    ctx.denoise(blocks, cw, lat, dclean, dmask, dtidx, dctx, dcos, dsin, sig, mode=mode)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    assert torch.isfinite(lat).all().item(), "non-finite latent"
+    steps = len(sig) - 1
+    f = flops(T, S)
+    block_flops = sum(f.values())
+    log(f"bench: denoise {steps} steps x {nb} blocks: {ms / 1e3:.3f} s, {ms / steps / nb:.2f} ms per block call")
+    res = {
+        "metric": "stage-1 denoise (8 Euler steps) over resident int8 blocks, seconds",
+        "value": round(ms / 1e3, 4), "unit": "s", "higher_is_better": False,
+        "n_gpus": 1, "steps": steps, "dtype": args.mode, "data": "synthetic",
+        "config": {"workload": "LTX-2.5 stage-1 denoising loop, int8 blocks resident", "tokens": T,
+                   "text_tokens": S, "blocks": nb, "sigmas": [float(v) for v in sig]},
+        "ms_per_block_call": round(ms / steps / nb, 3),
+        "block_tflops_in_loop": round(block_flops * steps * nb / (ms * 1e-3) / 1e12, 1),
+    }
+    for b in blocks:
+        b.free()
+    cw.free()
+    ctx.close()
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -100,6 +165,9 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=28672)
     ap.add_argument("--text", type=int, default=256)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--denoise", type=int, default=0, metavar="BLOCKS",
+                    help="instead of the block line: time the stage-1 denoising loop (8 Euler steps) over this "
+                         "many resident blocks (48 for the whole transformer) and print its own JSON line")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="run one plain device-to-device copy of this many MiB before the timed steps "
                          "(the known-size kernel that calibrates HBM byte counters)")
@@ -116,6 +184,8 @@ def main() -> int:
     from ltx_amd import synth
 
     T, S = args.tokens, args.text
+    if args.denoise:
+        return denoise_bench(args)
     t0 = time.time()
     bt = synth.make_block(0, seed=1, dist="t3", classes=("qkv", "ff", "out"), scale_dtype="F16")
     inp = synth.make_inputs(T, S, sigma=0.7)
