@@ -82,6 +82,24 @@ const char* ltx_version(void);
 int ltx_block_weights_from_blob(ltx_ctx* ctx, const void* mem, uint64_t mem_bytes, const char* manifest_json,
                                 int64_t block_idx, ltx_block_weights** out);
 
+/* Streaming form of ltx_block_weights_from_blob for a ring consumer
+ * (ltx/loader.zig:133-172 and the ring of :176-321, with one DMA per blob):
+ * enqueues on `stream` one hipMemcpyAsync of the whole blob image `mem`
+ * (pinned host memory such as a ring slot, for the copy to be asynchronous)
+ * into the context's staging buffer, then kernels that carve it into the
+ * device form (fused projections, weights as q + 128, scale pairs, widened
+ * biases and norm weights), and returns at once. The manifest is parsed and
+ * checked on the host first, with the same errors as the synchronous call.
+ * `reuse`: NULL for a new handle, or a handle of the same layout whose
+ * buffers are overwritten with no allocation (the caller orders this after
+ * the last kernel reading it). The caller keeps `mem` unchanged until
+ * `stream` has passed this call (record an event after it), and does not run
+ * two streaming uploads of one context on different streams at once (they
+ * share the staging buffer). */
+int ltx_block_weights_from_blob_async(ltx_ctx* ctx, const void* mem, uint64_t mem_bytes, const char* manifest_json,
+                                      int64_t block_idx, ltx_block_weights* reuse, void* stream,
+                                      ltx_block_weights** out);
+
 /* Upload one block from host pointers: base[LTX_W_COUNT] (bf16 bits / f32),
  * q8[LTX_Q_COUNT] int8 [O][I] or NULL, q8s[LTX_Q_COUNT] scales [O][I/128]
  * (f32, or f16 when scale_f16). */

@@ -87,6 +87,7 @@ struct ltx_ctx {
     ltx::DevBuf ws;
     ltx::DevBuf op_pairs;  // scale pairs of the last ltx_op_linear_q8 call (f16 scales)
     ltx::DevBuf op_q;      // its weights as bytes q + 128
+    ltx::DevBuf blob_stage;  // device copy of the blob image of the last streaming upload
     ltx::DevBuf core_ws;   // conditioning MLP rows
     ltx::DevBuf tail_ws;   // normed rows of ltx_core_tail
     ltx::DevBuf dn_ws;     // the denoising loop's activations

@@ -177,6 +177,7 @@ void ltx_destroy(ltx_ctx* c) {
     c->ws.free_();
     c->op_pairs.free_();
     c->op_q.free_();
+    c->blob_stage.free_();
     c->core_ws.free_();
     c->tail_ws.free_();
     c->dn_ws.free_();

@@ -213,8 +213,17 @@ struct Entry {
     uint64_t offset, nbytes;
 };
 
-ltx_block_weights* upload_blob(ltx_ctx* c, const void* mem, uint64_t mem_bytes, const char* manifest, int64_t block) {
-    if (!mem || !manifest) throw Error("NULL blob or manifest");
+// Offsets of one block's entries within its blob image (findEntry,
+// ltx/loader.zig:100-129, with the dtype and size checks of buildBlockBufs /
+// buildQuantBufs). q8 offsets are -1 where the companion is absent.
+struct BlobLayout {
+    uint64_t base[LTX_W_COUNT];
+    int64_t q8[LTX_Q_COUNT], q8s[LTX_Q_COUNT];
+    int sf16;
+};
+
+static BlobLayout parse_layout(uint64_t mem_bytes, const char* manifest, int64_t block) {
+    if (!manifest) throw Error("NULL manifest");
     json::Value m = json::parse(manifest);
     std::unordered_map<std::string, Entry> ents;
     for (const auto& e : m.at("entries").arr) {
@@ -222,25 +231,23 @@ ltx_block_weights* upload_blob(ltx_ctx* c, const void* mem, uint64_t mem_bytes, 
         if (en.offset + en.nbytes > mem_bytes) throw Error("manifest entry beyond the blob: " + e.at("name").as_str());
         ents[normalize_name(e.at("name").as_str())] = en;
     }
-    const char* bytes = (const char*)mem;
     auto find = [&](const std::string& want) -> const Entry* {
         auto it = ents.find(want);
         return it == ents.end() ? nullptr : &it->second;
     };
+    BlobLayout L;
     const std::string pre = "transformer_blocks_" + std::to_string(block) + "_";
-    const void* base[LTX_W_COUNT];
     for (int i = 0; i < LTX_W_COUNT; i++) {
         const Entry* e = find(pre + kBaseStems[i]);
         if (!e) throw Error("blob " + std::to_string(block) + ": no entry named " + pre + kBaseStems[i]);
         bool f32 = i == LTX_W_SST || i == LTX_W_PSST;
         if (e->dtype != (f32 ? "F32" : "BF16")) throw Error("unexpected dtype " + e->dtype + " for " + kBaseStems[i]);
         if (e->nbytes != base_numel(i) * (f32 ? 4 : 2)) throw Error(std::string("size mismatch for ") + kBaseStems[i]);
-        base[i] = bytes + e->offset;
+        L.base[i] = e->offset;
     }
-    const int8_t* q8[LTX_Q_COUNT] = {};
-    const void* q8s[LTX_Q_COUNT] = {};
     int sf16 = -1;
     for (int qi = 0; qi < LTX_Q_COUNT; qi++) {
+        L.q8[qi] = L.q8s[qi] = -1;
         std::string stem = pre + kBaseStems[kQBase[qi]];
         const Entry* eq = find(stem + "_q8");
         const Entry* es = find(stem + "_q8scale");
@@ -253,10 +260,171 @@ ltx_block_weights* upload_blob(ltx_ctx* c, const void* mem, uint64_t mem_bytes, 
         if (sf16 >= 0 && f16 != sf16) throw Error("mixed q8scale dtypes in one blob");
         sf16 = f16;
         if (es->nbytes != (uint64_t)O * (I / LTX_GROUP) * (f16 ? 2 : 4)) throw Error("bad q8scale size " + stem);
-        q8[qi] = (const int8_t*)(bytes + eq->offset);
-        q8s[qi] = bytes + es->offset;
+        L.q8[qi] = (int64_t)eq->offset;
+        L.q8s[qi] = (int64_t)es->offset;
     }
-    return upload(c, base, q8, q8s, sf16 < 0 ? 0 : sf16);
+    L.sf16 = sf16 < 0 ? 0 : sf16;
+    return L;
+}
+
+ltx_block_weights* upload_blob(ltx_ctx* c, const void* mem, uint64_t mem_bytes, const char* manifest, int64_t block) {
+    if (!mem || !manifest) throw Error("NULL blob or manifest");
+    const BlobLayout L = parse_layout(mem_bytes, manifest, block);
+    const char* bytes = (const char*)mem;
+    const void* base[LTX_W_COUNT];
+    for (int i = 0; i < LTX_W_COUNT; i++) base[i] = bytes + L.base[i];
+    const int8_t* q8[LTX_Q_COUNT] = {};
+    const void* q8s[LTX_Q_COUNT] = {};
+    for (int qi = 0; qi < LTX_Q_COUNT; qi++)
+        if (L.q8[qi] >= 0) {
+            q8[qi] = (const int8_t*)(bytes + L.q8[qi]);
+            q8s[qi] = bytes + L.q8s[qi];
+        }
+    return upload(c, base, q8, q8s, L.sf16);
+}
+
+// ---- streaming upload: one DMA of the blob image, carved on the device ----
+//
+// The same device form as upload(), built by kernels from the blob image in
+// the context's staging area: int8 parts flipped to q + 128 into the fused
+// projection, scales copied and paired, bf16 biases / norm weights widened,
+// f16 copies converted. Everything is enqueued on one stream.
+struct DevCarve {
+    ltx_ctx* c;
+    hipStream_t st;
+    const char* img;  // device copy of the blob
+    bool reuse;
+
+    void ensure(DevBuf& d, size_t n) {
+        if (reuse) {
+            if (d.bytes != n) throw Error("the reused weights handle has a different layout");
+        } else {
+            d.alloc(n);
+        }
+    }
+    void copy(void* dst, uint64_t off, size_t n) {
+        HIPC(hipMemcpyAsync(dst, img + off, n, hipMemcpyDeviceToDevice, st));
+    }
+    void flip(void* dst, uint64_t off, size_t n) {  // n bytes, a multiple of 4
+        LtxFlipArgs a{(const uint32_t*)(img + off), (uint32_t*)dst, n / 4};
+        c->launch("ltx_q8_flip", (unsigned)((n / 4 + 255) / 256), 1, 1, 256, &a, st);
+    }
+    void cvt(const void* src, void* dst, size_t n, int to_f16) {  // bf16 -> f32 (0) or f16 (1)
+        LtxCvtArgs a{(const uint16_t*)src, dst, n, to_f16};
+        c->launch("ltx_cvt_bf16", (unsigned)((n + 255) / 256), 1, 1, 256, &a, st);
+    }
+
+    void proj(LtxProj& p, const BlobLayout& L, std::initializer_list<int> qids, int K, bool want_f16_copy) {
+        std::vector<int> ids(qids);
+        bool all_q8 = true;
+        for (int qi : ids) all_q8 = all_q8 && L.q8[qi] >= 0;
+        if (reuse && (p.q8 != all_q8 || (all_q8 && p.scale_f16 != L.sf16)))
+            throw Error("the reused weights handle has a different layout");
+        std::vector<int> Ns;
+        p.K = K;
+        p.N = 0;
+        for (int qi : ids) {
+            int O, I;
+            q_dims(qi, O, I);
+            Ns.push_back(O);
+            p.N += O;
+        }
+        p.q8 = all_q8;
+        p.scale_f16 = L.sf16;
+        const size_t G = K / LTX_GROUP, ss = L.sf16 ? 2 : 4;
+        if (all_q8) {
+            ensure(p.q, (size_t)p.N * K);
+            ensure(p.s, (size_t)p.N * G * ss);
+            size_t r = 0;
+            for (size_t j = 0; j < ids.size(); j++) {
+                flip((char*)p.q.p + r * K, (uint64_t)L.q8[ids[j]], (size_t)Ns[j] * K);
+                copy((char*)p.s.p + r * G * ss, (uint64_t)L.q8s[ids[j]], (size_t)Ns[j] * G * ss);
+                r += Ns[j];
+            }
+            p.qflip = true;
+            if (L.sf16) {
+                ensure(p.s2, G * p.N * 4);
+                LtxPairArgs pa{(const uint16_t*)p.s.p, (uint32_t*)p.s2.p, p.N, (int)G};
+                c->launch("ltx_scale_pairs", (unsigned)((G * p.N + 255) / 256), 1, 1, 256, &pa, st);
+            }
+        } else {
+            ensure(p.w_bf16, (size_t)p.N * K * 2);
+            size_t r = 0;
+            for (size_t j = 0; j < ids.size(); j++) {
+                copy((char*)p.w_bf16.p + r * K * 2, L.base[kQBase[ids[j]]], (size_t)Ns[j] * K * 2);
+                r += Ns[j];
+            }
+            if (want_f16_copy) {
+                ensure(p.w_f16, (size_t)p.N * K * 2);
+                cvt(p.w_bf16.p, p.w_f16.p, (size_t)p.N * K, 1);
+            }
+        }
+        bool has_bias = false;
+        for (int qi : ids) has_bias = has_bias || (kQBase[qi] != LTX_W_FF1_W && kQBase[qi] != LTX_W_FF2_W);
+        if (has_bias) {
+            ensure(p.bias, (size_t)p.N * 4);
+            size_t r = 0;
+            for (size_t j = 0; j < ids.size(); j++) {
+                const int bw = kQBase[ids[j]];
+                if (bw == LTX_W_FF1_W || bw == LTX_W_FF2_W) throw Error("mixed biased and bias-free parts");
+                cvt(img + L.base[bw + 1], (float*)p.bias.p + r, (size_t)Ns[j], 0);
+                r += Ns[j];
+            }
+        }
+    }
+    void gate(LtxProj& p, const BlobLayout& L, int wi) {
+        p.N = LTX_H;
+        p.K = LTX_D;
+        const size_t n = (size_t)LTX_H * LTX_D;
+        ensure(p.w_bf16, n * 2);
+        copy(p.w_bf16.p, L.base[wi], n * 2);
+        ensure(p.w_f16, n * 2);
+        cvt(p.w_bf16.p, p.w_f16.p, n, 1);
+        ensure(p.bias, LTX_H * 4);
+        cvt(img + L.base[wi + 1], p.bias.p, LTX_H, 0);
+    }
+};
+
+ltx_block_weights* upload_blob_async(ltx_ctx* c, const void* mem, uint64_t mem_bytes, const char* manifest,
+                                     int64_t block, ltx_block_weights* reuse, hipStream_t st) {
+    if (!mem || !manifest) throw Error("NULL blob or manifest");
+    const BlobLayout L = parse_layout(mem_bytes, manifest, block);
+    HIPC(hipSetDevice(c->device));
+    if (c->blob_stage.bytes < mem_bytes) c->blob_stage.alloc(mem_bytes);
+    // the one DMA of the whole image (asynchronous when `mem` is pinned)
+    HIPC(hipMemcpyAsync(c->blob_stage.p, mem, mem_bytes, hipMemcpyHostToDevice, st));
+    ltx_block_weights* w = reuse ? reuse : new ltx_block_weights();
+    try {
+        DevCarve d{c, st, (const char*)c->blob_stage.p, reuse != nullptr};
+        d.proj(w->qkv1, L, {LTX_Q_Q1, LTX_Q_K1, LTX_Q_V1}, LTX_D, true);
+        d.proj(w->o1, L, {LTX_Q_O1}, LTX_D, true);
+        d.proj(w->q2, L, {LTX_Q_Q2}, LTX_D, true);
+        d.proj(w->kv2, L, {LTX_Q_K2, LTX_Q_V2}, LTX_D, true);
+        d.proj(w->o2, L, {LTX_Q_O2}, LTX_D, true);
+        d.proj(w->f1, L, {LTX_Q_F1}, LTX_D, true);
+        d.proj(w->f2, L, {LTX_Q_F2}, LTX_FF, true);
+        d.gate(w->g1, L, LTX_W_G1_W);
+        d.gate(w->g2, L, LTX_W_G2_W);
+        auto norm = [&](DevBuf& b, int wi) {
+            d.ensure(b, (size_t)LTX_D * 4);
+            d.cvt(d.img + L.base[wi], b.p, LTX_D, 0);
+        };
+        norm(w->qn1, LTX_W_QN1);
+        norm(w->kn1, LTX_W_KN1);
+        norm(w->qn2, LTX_W_QN2);
+        norm(w->kn2, LTX_W_KN2);
+        d.ensure(w->sst, 9 * (size_t)LTX_D * 4);
+        d.copy(w->sst.p, L.base[LTX_W_SST], 9 * (size_t)LTX_D * 4);
+        d.ensure(w->psst, 2 * (size_t)LTX_D * 4);
+        d.copy(w->psst.p, L.base[LTX_W_PSST], 2 * (size_t)LTX_D * 4);
+        w->bytes = proj_bytes(w->qkv1) + proj_bytes(w->o1) + proj_bytes(w->q2) + proj_bytes(w->kv2) +
+                   proj_bytes(w->o2) + proj_bytes(w->f1) + proj_bytes(w->f2) + proj_bytes(w->g1) + proj_bytes(w->g2) +
+                   w->qn1.bytes * 4 + w->sst.bytes + w->psst.bytes;
+    } catch (...) {
+        if (!reuse) delete w;
+        throw;
+    }
+    return w;
 }
 
 }  // namespace ltx
@@ -277,6 +445,15 @@ int ltx_block_weights_from_blob(ltx_ctx* c, const void* mem, uint64_t mem_bytes,
     LTX_GUARD(c, {
         if (!c || !out) throw ltx::Error("NULL context or out");
         *out = ltx::upload_blob(c, mem, mem_bytes, manifest_json, block_idx);
+    })
+}
+
+int ltx_block_weights_from_blob_async(ltx_ctx* c, const void* mem, uint64_t mem_bytes, const char* manifest_json,
+                                      int64_t block_idx, ltx_block_weights* reuse, void* stream,
+                                      ltx_block_weights** out) {
+    LTX_GUARD(c, {
+        if (!c || !out) throw ltx::Error("NULL context or out");
+        *out = ltx::upload_blob_async(c, mem, mem_bytes, manifest_json, block_idx, reuse, (hipStream_t)stream);
     })
 }
 

@@ -202,6 +202,16 @@ extern "C" __global__ void __launch_bounds__(256) ltx_dequant_f16(const LtxDequa
 extern "C" __global__ void __launch_bounds__(256) ltx_dequant_bf16(const LtxDequantArgs a) { dequant_body<__bf16>(a); }
 
 // Scale pairs for the LDS-DMA int8 GEMM: out[g][n] = s[n][g] in both halves.
+extern "C" __global__ void __launch_bounds__(256) ltx_cvt_bf16(const LtxCvtArgs a) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.n) return;
+    const float v = __builtin_bit_cast(float, (uint32_t)a.in[i] << 16);
+    if (a.to_f16)
+        ((_Float16*)a.out)[i] = (_Float16)v;
+    else
+        ((float*)a.out)[i] = v;
+}
+
 extern "C" __global__ void __launch_bounds__(256) ltx_q8_flip(const LtxFlipArgs a) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i < a.n) a.out[i] = a.in[i] ^ 0x80808080u;

@@ -124,6 +124,15 @@ typedef struct {
     int scale_f16;
 } LtxDequantArgs;
 
+// bf16 -> f32 (to_f16 = 0) or f16 (to_f16 = 1, round to nearest even), n
+// elements.
+typedef struct {
+    const uint16_t* in;
+    void* out;
+    size_t n;
+    int to_f16;
+} LtxCvtArgs;
+
 // int8 weights -> bytes q + 128 (XOR 0x80 per byte), n words of 4 bytes.
 typedef struct {
     const uint32_t* in;

@@ -46,6 +46,7 @@ def lib() -> C.CDLL:
         "ltx_version": (C.c_char_p, []),
         "ltx_block_weights_from_blob": (i32, [vp, vp, u64, C.c_char_p, i64, C.POINTER(vp)]),
         "ltx_block_weights_from_host": (i32, [vp, C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), i32, C.POINTER(vp)]),
+        "ltx_block_weights_from_blob_async": (i32, [vp, vp, u64, C.c_char_p, i64, vp, vp, C.POINTER(vp)]),
         "ltx_block_weights_free": (None, [vp, vp]),
         "ltx_block_weights_bytes": (u64, [vp]),
         "ltx_block_forward": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, vp, vp, vp, i32, vp, i32, vp]),
@@ -211,6 +212,18 @@ class Context:
                                                       manifest_json.encode(), block, C.byref(h)),
                     "ltx_block_weights_from_blob")
         return Weights(self, h.value)
+
+    def upload_blob_async(self, mem_ptr: int, nbytes: int, manifest_json: str, block: int, reuse: Weights | None = None,
+                          stream=None) -> Weights:
+        """Streaming upload from `mem_ptr` (pinned host memory, e.g. a ring
+        slot) on `stream`; returns at once. Keep the memory unchanged until
+        the stream passes this call."""
+        st = stream.cuda_stream if stream is not None else _current_stream()
+        h = C.c_void_p()
+        self._check(lib().ltx_block_weights_from_blob_async(self.handle, mem_ptr, nbytes, manifest_json.encode(),
+                                                            block, reuse.handle if reuse else None, st, C.byref(h)),
+                    "ltx_block_weights_from_blob_async")
+        return reuse if reuse is not None else Weights(self, h.value)
 
     # ---- forward ----
     def forward(self, w: Weights, x, tstab, tidx, ctx, pts2, cos, sin, y, mode: int = MODE_F16, stream=None):
