@@ -15,10 +15,23 @@ __device__ void norm_mod_body(const LtxNormArgs& a) {
     float4 v[4];
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        v[i] = x[threadIdx.x + 256 * i];
-        ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    for (int i = 0; i < 4; i++) v[i] = x[threadIdx.x + 256 * i];
+    // the modulation rows do not depend on the row statistics: loaded before
+    // the reduction so their latency overlaps it
+    float4 sct[4], scs[4], sht[4], shs[4];
+    if (a.isc >= 0) {
+        const int r = a.ada.tidx[row];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = 4 * (threadIdx.x + 256 * i);
+            sct[i] = *(const float4*)(a.ada.tstab + ((size_t)r * 9 + a.isc) * LTX_D + c);
+            scs[i] = *(const float4*)(a.ada.sst + (size_t)a.isc * LTX_D + c);
+            sht[i] = *(const float4*)(a.ada.tstab + ((size_t)r * 9 + a.ish) * LTX_D + c);
+            shs[i] = *(const float4*)(a.ada.sst + (size_t)a.ish * LTX_D + c);
+        }
     }
+#pragma unroll
+    for (int i = 0; i < 4; i++) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
     ss = block_sum256(ss, red);
     float inv = 1.0f / sqrtf(ss * (1.0f / LTX_D) + 1e-6f);
 #pragma unroll
@@ -26,13 +39,8 @@ __device__ void norm_mod_body(const LtxNormArgs& a) {
         int c = 4 * (threadIdx.x + 256 * i);
         float o[4] = {v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv};
         if (a.isc >= 0) {
-            int r = a.ada.tidx[row];
-            const float4 sc_t = *(const float4*)(a.ada.tstab + ((size_t)r * 9 + a.isc) * LTX_D + c);
-            const float4 sc_s = *(const float4*)(a.ada.sst + (size_t)a.isc * LTX_D + c);
-            const float4 sh_t = *(const float4*)(a.ada.tstab + ((size_t)r * 9 + a.ish) * LTX_D + c);
-            const float4 sh_s = *(const float4*)(a.ada.sst + (size_t)a.ish * LTX_D + c);
-            float sc[4] = {sc_t.x + sc_s.x, sc_t.y + sc_s.y, sc_t.z + sc_s.z, sc_t.w + sc_s.w};
-            float sh[4] = {sh_t.x + sh_s.x, sh_t.y + sh_s.y, sh_t.z + sh_s.z, sh_t.w + sh_s.w};
+            float sc[4] = {sct[i].x + scs[i].x, sct[i].y + scs[i].y, sct[i].z + scs[i].z, sct[i].w + scs[i].w};
+            float sh[4] = {sht[i].x + shs[i].x, sht[i].y + shs[i].y, sht[i].z + shs[i].z, sht[i].w + shs[i].w};
 #pragma unroll
             for (int j = 0; j < 4; j++) o[j] = o[j] * (sc[j] + 1.0f) + sh[j];
         }
@@ -102,22 +110,37 @@ __device__ void qknorm_body(const LtxQkNormArgs& a) {
         lo[j] = p.x; lo[j + 1] = p.y; lo[j + 2] = p.z; lo[j + 3] = p.w;
         hi[j] = q.x; hi[j + 1] = q.y; hi[j + 2] = q.z; hi[j + 3] = q.w;
     }
-#pragma unroll
-    for (int j = 0; j < 8; j++) ss += lo[j] * lo[j] + hi[j] * hi[j];
-    ss = block_sum256(ss, red);
-    float inv = 1.0f / sqrtf(ss * (1.0f / LTX_D) + 1e-6f);
+    // norm weights and RoPE rows do not depend on the row statistics: loaded
+    // before the reduction so their latency overlaps it
     const float* wl = a.w + h * LTX_HD + f0;
+    float wlo[8], whi[8], cs[8], sn[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        lo[j] = lo[j] * inv * wl[j];
-        hi[j] = hi[j] * inv * wl[64 + j];
+        wlo[j] = wl[j];
+        whi[j] = wl[64 + j];
     }
     if (a.cos) {
         const float* cr = a.cos + ((size_t)row * LTX_H + h) * 64 + f0;
         const float* sr = a.sin + ((size_t)row * LTX_H + h) * 64 + f0;
 #pragma unroll
+        for (int j = 0; j < 8; j += 4) {
+            *(float4*)(cs + j) = *(const float4*)(cr + j);
+            *(float4*)(sn + j) = *(const float4*)(sr + j);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) ss += lo[j] * lo[j] + hi[j] * hi[j];
+    ss = block_sum256(ss, red);
+    float inv = 1.0f / sqrtf(ss * (1.0f / LTX_D) + 1e-6f);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        lo[j] = lo[j] * inv * wlo[j];
+        hi[j] = hi[j] * inv * whi[j];
+    }
+    if (a.cos) {
+#pragma unroll
         for (int j = 0; j < 8; j++) {
-            float c = cr[j], s = sr[j], x0 = lo[j], x1 = hi[j];
+            float c = cs[j], s = sn[j], x0 = lo[j], x1 = hi[j];
             lo[j] = x0 * c - x1 * s;
             hi[j] = x1 * c + x0 * s;
         }
