@@ -7,7 +7,10 @@
  * Status convention as ltx_block.h: non-zero = success. Error names follow
  * the reference's error set and appear in the error text:
  *   BlobSizeMismatch, Misaligned, LayoutGap, TrailingBytes, MissingEntry,
- *   BlobDigestMismatch, ScheduleOutOfRange, SlotTooSmall, RingShutdown.
+ *   BlobDigestMismatch, ScheduleOutOfRange, SlotTooSmall, RingShutdown,
+ * plus FormatVersion: packer_version must be 1 (the reference format: F32
+ * scales, int8 q/k/v and ff only) or 2 (adds F16 scales and int8
+ * out-projections), and a version-1 manifest may not use version-2 entries.
  */
 #ifndef LTX_LOADER_H
 #define LTX_LOADER_H

@@ -26,6 +26,7 @@
 namespace ltx {
 std::string sha256_hex(const void* data, size_t n);
 std::string normalize_name(const std::string& n);
+void check_format_version(const json::Value& m);
 }  // namespace ltx
 
 static thread_local std::string g_loader_err;
@@ -174,6 +175,11 @@ int ltx_blob_open(const char* dir, ltx_blob** out) {
         std::string d(dir);
         b->manifest_text = read_file(d + "/blob_manifest.json");
         ltx::json::Value m = ltx::json::parse(b->manifest_text.c_str());
+        try {
+            ltx::check_format_version(m);
+        } catch (const std::exception& ex) {
+            fail(ex.what());
+        }
         b->total_bytes = (uint64_t)m.at("total_bytes").as_int();
         b->align = (uint64_t)m.at("align").as_int();
         b->block = m.at("block").as_int();

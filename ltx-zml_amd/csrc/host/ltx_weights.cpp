@@ -213,6 +213,26 @@ struct Entry {
     uint64_t offset, nbytes;
 };
 
+// packer_version 1 is the reference format (F32 scales; int8 companions for
+// q/k/v and ff only); version 2 adds F16 scale entries and int8
+// out-projections. A version-1 manifest carrying either is refused.
+void check_format_version(const json::Value& m) {
+    const json::Value* pv = m.get("packer_version");
+    const int64_t v = pv ? pv->as_int() : 1;
+    if (v != 1 && v != 2) throw Error("FormatVersion: unsupported packer_version " + std::to_string(v));
+    if (v == 2) return;
+    for (const auto& e : m.at("entries").arr) {
+        const std::string& n = e.at("name").as_str();
+        auto ends = [&](const std::string& suf) {
+            return n.size() >= suf.size() && n.compare(n.size() - suf.size(), suf.size(), suf) == 0;
+        };
+        if (ends("::q8scale") && e.at("dtype").as_str() == "F16")
+            throw Error("FormatVersion: version-1 manifest with F16 scales (" + n + ")");
+        if (ends("attn1.to_out.0.weight::q8") || ends("attn2.to_out.0.weight::q8"))
+            throw Error("FormatVersion: version-1 manifest with an int8 out-projection (" + n + ")");
+    }
+}
+
 // Offsets of one block's entries within its blob image (findEntry,
 // ltx/loader.zig:100-129, with the dtype and size checks of buildBlockBufs /
 // buildQuantBufs). q8 offsets are -1 where the companion is absent.
@@ -225,6 +245,7 @@ struct BlobLayout {
 static BlobLayout parse_layout(uint64_t mem_bytes, const char* manifest, int64_t block) {
     if (!manifest) throw Error("NULL manifest");
     json::Value m = json::parse(manifest);
+    check_format_version(m);
     std::unordered_map<std::string, Entry> ents;
     for (const auto& e : m.at("entries").arr) {
         Entry en{e.at("dtype").as_str(), (uint64_t)e.at("offset").as_int(), (uint64_t)e.at("nbytes").as_int()};

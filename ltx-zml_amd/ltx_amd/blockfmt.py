@@ -13,8 +13,13 @@ byte-compatible with its loader:
   and whole-blob sha256 (tools/pack_block.py:33-95);
 - ``normalize_name`` (ltx/loader.zig:100-119).
 
-Scale entries may also be written as F16 (``scale_dtype="F16"``), the
-half-size variant the GEMM kernels read natively; the reference format is F32.
+Format versions. ``packer_version`` 1 is the reference format exactly
+(F32 scales, int8 companions for the q/k/v and ff classes only). A blob that
+uses either extension — F16 scale entries (``scale_dtype="F16"``, the
+half-size form the GEMM kernels read natively) or int8 companions of the
+out-projections (class "out") — is written as version 2; every version-1
+blob still packs byte for byte as the reference tool does, and readers
+refuse a version-1 manifest that carries an extension (``check_version``).
 """
 from __future__ import annotations
 
@@ -25,7 +30,8 @@ from dataclasses import dataclass
 import numpy as np
 
 D, H, FF, GROUP = 4096, 32, 16384, 128
-PACKER_VERSION = 1
+PACKER_VERSION = 1  # the reference format (tools/pack_block.py:27)
+PACKER_VERSION_EXT = 2  # F16 scales and / or int8 out-projections
 ALIGN = 64
 
 # (field, tensor suffix after "transformer_blocks.{i}.", shape, dtype) in
@@ -153,11 +159,38 @@ def pack(bt: BlockTensors, repo: str = "synthetic", revision: str = "synthetic",
     return pack_entries(entries, bt.block, repo, revision, source_file, model_version, packer_commit)
 
 
+_OUT_SUFFIXES = ("attn1.to_out.0.weight", "attn2.to_out.0.weight")
+
+
+def _extensions(entries) -> list:
+    """Version-2 features among (name, dtype) pairs."""
+    ext = []
+    for name, dtype in entries:
+        if name.endswith("::q8scale") and dtype == "F16":
+            ext.append(f"F16 scales ({name})")
+        if name.endswith("::q8") and name[:-4].endswith(_OUT_SUFFIXES):
+            ext.append(f"int8 out-projection ({name})")
+    return ext
+
+
+def check_version(manifest: dict) -> None:
+    """packer_version 1 or 2; a version-1 manifest may not use the
+    version-2 extensions."""
+    v = manifest.get("packer_version", PACKER_VERSION)
+    if v not in (PACKER_VERSION, PACKER_VERSION_EXT):
+        raise ValueError(f"FormatVersion: unsupported packer_version {v}")
+    ext = _extensions((e["name"], e["dtype"]) for e in manifest["entries"])
+    if v == PACKER_VERSION and ext:
+        raise ValueError(f"FormatVersion: version-1 manifest with a version-2 extension: {ext[0]}")
+
+
 def pack_entries(entries: list, block: int, repo: str, revision: str, source_file: str, model_version: str,
                  packer_commit: str) -> tuple[bytes, dict]:
     """Canonical blob from (name, bytes, dtype, shape) entries: name-sorted,
-    64-byte aligned with zero fill (tools/pack_block.py:54-91)."""
+    64-byte aligned with zero fill (tools/pack_block.py:54-91). Version 2
+    when an extension is present, else 1."""
     entries = sorted(entries, key=lambda t: t[0])
+    version = PACKER_VERSION_EXT if _extensions((n, d) for n, _, d, _ in entries) else PACKER_VERSION
     blob = bytearray()
     mentries = []
     for name, data, dtype, shape in entries:
@@ -168,7 +201,7 @@ def pack_entries(entries: list, block: int, repo: str, revision: str, source_fil
         mentries.append({"name": name, "dtype": dtype, "shape": shape, "offset": off, "nbytes": len(data),
                          "sha256": hashlib.sha256(data).hexdigest()})
     manifest = {
-        "packer_version": PACKER_VERSION, "packer_commit": packer_commit, "align": ALIGN, "block": block,
+        "packer_version": version, "packer_commit": packer_commit, "align": ALIGN, "block": block,
         "repo": repo, "revision": revision, "source_file": source_file, "model_version": model_version,
         "total_bytes": len(blob), "blob_sha256": hashlib.sha256(bytes(blob)).hexdigest(), "entries": mentries,
     }
@@ -192,6 +225,7 @@ def check_layout(manifest: dict) -> None:
 def unpack(blob: bytes, manifest: dict, block: int | None = None) -> BlockTensors:
     """Inverse of ``pack``: numpy views of every entry (buildBlockBufs /
     buildQuantBufs lookups, ltx/loader.zig:133-172)."""
+    check_version(manifest)
     block = manifest["block"] if block is None else block
     byname = {normalize_name(e["name"]): e for e in manifest["entries"]}
     mv = memoryview(blob)

@@ -235,3 +235,47 @@ def test_ring_reader_error_reaches_consumer(tmp_path):
     assert "BlobDigestMismatch" in L.ltx_loader_last_error().decode()
     L.ltx_ring_destroy(r)
     L.ltx_blob_close(h)
+
+
+# ---- format versions ----------------------------------------------------------
+
+def _tiny_entries(scale_dtype="F32", out_q8=False):
+    """A few named entries (small shapes) exercising the version rule."""
+    q = np.arange(256, dtype=np.int16).astype(np.int8).reshape(2, 128)
+    s = np.ones((2, 1), dtype=np.float16 if scale_dtype == "F16" else np.float32)
+    ents = [("transformer_blocks.0.attn1.to_q.weight", b"\x00" * 8, "BF16", [2, 2]),
+            ("transformer_blocks.0.attn1.to_q.weight::q8", q.tobytes(), "I8", [2, 128]),
+            ("transformer_blocks.0.attn1.to_q.weight::q8scale", s.tobytes(), scale_dtype, [2, 1])]
+    if out_q8:
+        ents += [("transformer_blocks.0.attn1.to_out.0.weight::q8", q.tobytes(), "I8", [2, 128]),
+                 ("transformer_blocks.0.attn1.to_out.0.weight::q8scale", s.tobytes(), scale_dtype, [2, 1])]
+    return ents
+
+
+@pytest.mark.parametrize("scale_dtype,out_q8,version", [("F32", False, 1), ("F16", False, 2), ("F32", True, 2),
+                                                        ("F16", True, 2)])
+def test_packer_version_follows_extensions(tmp_path, scale_dtype, out_q8, version):
+    blob, man = bf.pack_entries(_tiny_entries(scale_dtype, out_q8), 0, "r", "v", "f", "", "c")
+    assert man["packer_version"] == version
+    bf.check_version(man)
+    _write_blob(tmp_path / "ok", blob, man)
+    ok, h, err = _open(tmp_path / "ok")
+    assert ok, err
+    rt.lib().ltx_blob_close(h)
+
+
+def test_version1_manifest_with_extension_is_refused(tmp_path):
+    blob, man = bf.pack_entries(_tiny_entries("F16", True), 0, "r", "v", "f", "", "c")
+    for v, what in ((1, "version-1 manifest"), (3, "unsupported packer_version 3")):
+        m = dict(man, packer_version=v)
+        with pytest.raises(ValueError, match="FormatVersion"):
+            bf.check_version(m)
+        _write_blob(tmp_path / f"v{v}", blob, m)
+        ok, h, err = _open(tmp_path / f"v{v}")
+        assert not ok and "FormatVersion" in err and what in err
+
+
+def test_reference_golden_blob_is_version1():
+    man = json.loads((GOLD / "output" / "blob_manifest.json").read_text())
+    assert man["packer_version"] == bf.PACKER_VERSION == 1
+    bf.check_version(man)
