@@ -1,0 +1,114 @@
+"""The block at its full size (T = 28,672 tokens on the (14, 32, 64) grid,
+S = 256, every projection int8 with f16 scales, fp16 MFMA mode), checked
+where an f64 reference is affordable:
+
+- self-attention: 64 query rows (spread over the sequence) of the gated,
+  head-merged attention output (stage LTX_ST_ATTN1) against f64 softmax
+  attention over all 28,672 keys, computed from the kernel's own 16-bit
+  Q, K, V^T and f32 gate logits (stages Q1, K1, V1, GLOG1; Q carries
+  log2(e)/sqrt(128), divided back exactly here); gate rel-RMS <= 2e-3;
+- the FFN up-projection: 32 rows of gelu(ff_in . dq(W_f1)^T) (stage FF_H)
+  against f64 from the kernel's own 16-bit input rows (stage FF_IN);
+- size-independent properties of the whole block: finite output, two
+  forwards bit-identical, and zeroed residual gates returning x exactly.
+"""
+import numpy as np
+import pytest
+
+from conftest import say
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+import oracle  # noqa: E402
+from ltx_amd import blockfmt as bf  # noqa: E402
+from ltx_amd import runtime as rt  # noqa: E402
+from ltx_amd import synth  # noqa: E402
+
+T, S = 28672, 256
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.fixture(scope="module")
+def full():
+    bt = synth.make_block(0, seed=1, dist="t3", classes=("qkv", "ff", "out"), scale_dtype="F16")
+    inp = synth.make_inputs(T, S, sigma=0.7)
+    cos, sin = rt.rope_tables(inp["grid"])
+    return bt, inp, cos, sin
+
+
+def _run(ctx, w, inp, cos, sin):
+    y = torch.empty((T, 4096), dtype=torch.float32, device="cuda")
+    ctx.forward(w, dev(inp["x"]), dev(inp["tstab"]), dev(inp["tidx"]), dev(inp["ctx"]), dev(inp["pts2"]), dev(cos),
+                dev(sin), y, mode=rt.MODE_F16)
+    torch.cuda.synchronize()
+    return y
+
+
+def _stage(ctx, name, dtype, shape, rows=None):
+    t = ctx.stage(name).view(dtype).reshape(shape)
+    if rows is not None:
+        t = t[torch.from_numpy(rows).cuda()]
+    return t.cpu().numpy().astype(np.float64)
+
+
+def test_full_size_block(ctx, full):
+    bt, inp, cos, sin = full
+    say(f"full-size block T={T} S={S} f16: forward, determinism, attention and FFN rows")
+    w = ctx.upload(bt)
+    y1 = _run(ctx, w, inp, cos, sin)
+    assert torch.isfinite(y1).all().item()
+    # stages of this forward (rows picked on the device)
+    rows = np.linspace(0, T - 1, 64).astype(np.int64)
+    frows = np.linspace(3, T - 5, 32).astype(np.int64)
+    q = _stage(ctx, "q1", torch.float16, (32, T, 128)) / rt.ATTN_C
+    k = _stage(ctx, "k1", torch.float16, (32, T, 128))
+    vt = _stage(ctx, "v1", torch.float16, (32, 128, T))
+    glog = _stage(ctx, "glog1", torch.float32, (T, 32), rows)
+    att = _stage(ctx, "attn1", torch.float16, (T, 4096), rows)
+    ff_in = _stage(ctx, "ff_in", torch.float16, (T, 4096), frows)
+    ff_h = _stage(ctx, "ff_h", torch.float16, (T, 16384), frows)
+    y2 = _run(ctx, w, inp, cos, sin)
+    assert torch.equal(y1.view(torch.int32), y2.view(torch.int32)), "two forwards differ"
+    w.free()
+
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(128.0)))
+    want = np.empty((len(rows), 4096))
+    for h in range(32):
+        s = (q[h, rows] @ k[h].T) * scale  # [64, T]
+        p = np.exp(s - s.max(1, keepdims=True))
+        o = (p @ vt[h].T) / p.sum(1, keepdims=True)  # [64, 128]
+        want[:, 128 * h:128 * h + 128] = o * (2.0 / (1.0 + np.exp(-glog[:, h])))[:, None]
+    r_att = oracle.rel_rms(att, want)
+
+    wf = oracle.dequant(bt.q8["f1"], bt.q8s["f1"]).astype(np.float64)
+    hpre = ff_in @ wf.T
+    hw = 0.5 * hpre * (1 + np.tanh(np.sqrt(2 / np.pi) * (hpre + 0.044715 * hpre ** 3)))
+    r_ff = oracle.rel_rms(ff_h, hw)
+    print(f"full size: attention rows rel-RMS {r_att:.3e}, ff1+gelu rows rel-RMS {r_ff:.3e}", flush=True)
+    assert r_att <= 2e-3 and r_ff <= 2e-3
+
+
+def test_full_size_zero_gates_identity(ctx, full):
+    """sst rows 2, 5, 8 set to minus the tstab rows of the single mask row:
+    every residual gate is zero, so the block returns x exactly (as values:
+    x + v * 0 turns an input -0.0, of which the 117 M normal draws hold a
+    few, into +0.0)."""
+    bt, inp, cos, sin = full
+    say(f"full-size zero-gate identity T={T}")
+    inp1 = synth.make_inputs(T, S, sigma=0.7, striped=False)
+    b2 = bf.BlockTensors(0, dict(bt.base), bt.q8, bt.q8s)
+    sst = b2.base["sst"].copy()
+    for i in (2, 5, 8):
+        sst[i] = -inp1["tstab"][0, i]
+    b2.base["sst"] = sst
+    w = ctx.upload(b2)
+    y = _run(ctx, w, inp1, cos, sin)
+    w.free()
+    got = y.cpu().numpy()
+    assert np.isfinite(got).all() and np.array_equal(got, inp1["x"])
+    differ = got.view(np.uint32) != inp1["x"].view(np.uint32)
+    assert (inp1["x"][differ] == 0).all()  # only the sign of zeros may change
