@@ -326,8 +326,11 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.nsplit = 2 * LTX_D;
     gemm16(c, mode, w->qkv1, b.n_msa, T, LTX_D, LTX_EPI_QKV, g, st, "gemm:qkv1");
     gate16(c, mode, w->g1, b.n_msa, T, (float*)b.glog1, st);
-    qknorm16(c, mode, (const float*)b.qk32, 2 * LTX_D, w->qn1.p, cs, sn, b.qh1, T, kAttnC, st);
-    qknorm16(c, mode, (const float*)b.qk32 + LTX_D, 2 * LTX_D, w->kn1.p, cs, sn, b.kh1, T, 1.0f, st);
+    {  // q and k norms + RoPE in one pass (the RoPE rows read once)
+        LtxQkNorm2Args qa{(const float*)b.qk32, (const float*)w->qn1.p, (const float*)w->kn1.p, cs, sn, b.qh1, b.kh1,
+                          T, 2 * LTX_D, kAttnC, 1.0f};
+        c->launch(mode == LTX_MODE_BF16 ? "ltx_qknorm2_bf16" : "ltx_qknorm2_f16", T, 1, 1, 256, &qa, st);
+    }
     attn16(c, mode, b.qh1, b.kh1, b.vt1, (const float*)b.glog1, b.o1, T, T, true, st, "attn:self");
     g = LtxGemmArgs{};
     g.out = b.x_sa;

@@ -157,6 +157,76 @@ __device__ void qknorm_body(const LtxQkNormArgs& a) {
     *(u32x4*)(y + 64 + f0) = phi;
 }
 
+// q and k of one token together (same thread layout as qknorm_body), the
+// cos / sin rows loaded once for both.
+template <typename T>
+__device__ void qknorm2_body(const LtxQkNorm2Args& a) {
+    __shared__ float red[8];
+    const int row = blockIdx.x;
+    if (row >= a.rows) return;
+    const int h = threadIdx.x >> 3, f0 = (threadIdx.x & 7) * 8;
+    float lo[2][8], hi[2][8], cs[8], sn[8], wlo[2][8], whi[2][8];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const float* xr = a.x + (size_t)row * a.ldx + p * LTX_D + h * LTX_HD;
+#pragma unroll
+        for (int j = 0; j < 8; j += 4) {
+            *(float4*)(lo[p] + j) = *(const float4*)(xr + f0 + j);
+            *(float4*)(hi[p] + j) = *(const float4*)(xr + 64 + f0 + j);
+        }
+        const float* wl = (p ? a.wk : a.wq) + h * LTX_HD + f0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            wlo[p][j] = wl[j];
+            whi[p][j] = wl[64 + j];
+        }
+    }
+    const float* cr = a.cos + ((size_t)row * LTX_H + h) * 64 + f0;
+    const float* sr = a.sin + ((size_t)row * LTX_H + h) * 64 + f0;
+#pragma unroll
+    for (int j = 0; j < 8; j += 4) {
+        *(float4*)(cs + j) = *(const float4*)(cr + j);
+        *(float4*)(sn + j) = *(const float4*)(sr + j);
+    }
+    float ss[2] = {0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < 2; p++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) ss[p] += lo[p][j] * lo[p][j] + hi[p][j] * hi[p][j];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        ss[0] += __shfl_xor(ss[0], o, 64);
+        ss[1] += __shfl_xor(ss[1], o, 64);
+    }
+    const int wv = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        red[wv] = ss[0];
+        red[4 + wv] = ss[1];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const float tot = red[4 * p] + red[4 * p + 1] + red[4 * p + 2] + red[4 * p + 3];
+        const float inv = 1.0f / sqrtf(tot * (1.0f / LTX_D) + 1e-6f);
+        const float osc = p ? a.oscale_k : a.oscale_q;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float x0 = lo[p][j] * inv * wlo[p][j], x1 = hi[p][j] * inv * whi[p][j];
+            lo[p][j] = (x0 * cs[j] - x1 * sn[j]) * osc;
+            hi[p][j] = (x1 * cs[j] + x0 * sn[j]) * osc;
+        }
+        uint16_t* y = (uint16_t*)(p ? a.yk : a.yq) + ((size_t)h * a.rows + row) * LTX_HD;
+        const float* l = lo[p];
+        const float* u = hi[p];
+        *(u32x4*)(y + f0) = u32x4{pack2<T>(l[0], l[1]), pack2<T>(l[2], l[3]), pack2<T>(l[4], l[5]), pack2<T>(l[6], l[7])};
+        *(u32x4*)(y + 64 + f0) =
+            u32x4{pack2<T>(u[0], u[1]), pack2<T>(u[2], u[3]), pack2<T>(u[4], u[5]), pack2<T>(u[6], u[7])};
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) ltx_qknorm2_f16(const LtxQkNorm2Args a) { qknorm2_body<_Float16>(a); }
+extern "C" __global__ void __launch_bounds__(256) ltx_qknorm2_bf16(const LtxQkNorm2Args a) { qknorm2_body<__bf16>(a); }
+
 extern "C" __global__ void __launch_bounds__(256) ltx_qknorm_f16(const LtxQkNormArgs a) { qknorm_body<_Float16>(a); }
 extern "C" __global__ void __launch_bounds__(256) ltx_qknorm_bf16(const LtxQkNormArgs a) { qknorm_body<__bf16>(a); }
 

@@ -90,6 +90,21 @@ typedef struct {
     float oscale;       // applied before the 16-bit rounding (1, or the attention's exponent scale for Q)
 } LtxQkNormArgs;
 
+// The self-attention's q and k rows of one token in one pass (the RoPE rows
+// read once): q = x[row][0 .. D), k = x[row][D .. 2D).
+typedef struct {
+    const float* x;     // [rows][ldx] f32, q | k
+    const float* wq;    // [D] norm weights (f32)
+    const float* wk;
+    const float* cos;   // [rows][H][64]
+    const float* sin;
+    void* yq;           // [H][rows][HD]
+    void* yk;
+    int rows;
+    int ldx;
+    float oscale_q, oscale_k;
+} LtxQkNorm2Args;
+
 // Blockwise online-softmax attention with per-(token, head) gate.
 // q, k: [H][L][HD] 16-bit; vt: [H][HD][Lkv] 16-bit; glog: [Lq][H] f32 gate
 // logits (gate = 2*sigmoid); out: [Lq][D] 16-bit merged heads.
