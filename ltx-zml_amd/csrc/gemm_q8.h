@@ -190,35 +190,23 @@ struct Q8Gemm {
         for (int j = 0; j < NJ; j++) s2[j] = __builtin_bit_cast(f16x2, sn[j]);
     }
 
+    // One output tile per trip of a persistent loop: the grid is at most one
+    // workgroup per CU, and workgroup b takes tiles b, b + grid, ... (the same
+    // XCD and order as one workgroup per tile, without a dispatch and a drain
+    // of the epilogue's stores between tiles).
     __device__ __forceinline__ void run() {
         const int tid = threadIdx.x, lane = tid & 63;
         const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
         g = w >> 2;
         const int q = w & 3;
-        const TileIdx ti = tile_of(blockIdx.x, a.tiles_m, a.tiles_n);
-        const int m0 = ti.tm * 256, n0 = ti.tn * 256;
         nk = a.K / 64;
         ng = a.K / LTX_GROUP;
         ra_ = __builtin_amdgcn_make_buffer_rsrc((void*)a.a, 0, (int)((uint32_t)a.M * (uint32_t)a.lda * 2u), Q8_RSRC_W3);
         rb_ = __builtin_amdgcn_make_buffer_rsrc((void*)a.b, 0, (int)((uint32_t)a.N * (uint32_t)a.K), Q8_RSRC_W3);
         rs_ = __builtin_amdgcn_make_buffer_rsrc((void*)a.scales, 0, (int)((uint32_t)ng * (uint32_t)a.N * 4u),
                                                 Q8_RSRC_W3);
-        // DMA sources. A: instruction i of wave w fills rows 8 (4 w + i) .. +7,
-        // 8 lanes a row; W: rows 16 (2 w + i) .. +15, 4 lanes a row.
-        {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int tr = 8 * (4 * w + i) + (lane >> 3);  // row within the tile
-                const int c = (lane & 7) ^ ((tr >> 1) & 7);
-                const int row = min(m0 + tr, a.M - 1);
-                ga[i] = (uint32_t)row * (uint32_t)a.lda * 2u + 16u * c;
-            }
-            const int nr = lane >> 2, nc = (lane & 3) ^ ((lane >> 4) & 3);
-#pragma unroll
-            for (int i = 0; i < 2; i++) gb[i] = (uint32_t)(n0 + 16 * (2 * w + i) + nr) * (uint32_t)a.K + 16u * nc;
-            la = 4096 * w;
-            lb = 2048 * w;
-        }
+        la = 4096 * w;
+        lb = 2048 * w;
         // fragment reads: A row 128 g + 32 i + lane % 32, chunks 4 h + t;
         // W row 64 q + 32 j + lane % 32, chunks 2 h + c (h = lane / 32)
         {
@@ -227,44 +215,70 @@ struct Q8Gemm {
             for (int t = 0; t < 4; t++) offa[t] = (128 * g + r) * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7));
 #pragma unroll
             for (int c = 0; c < 2; c++) offb[c] = (64 * q + r) * 64 + 16 * ((2 * h + c) ^ ((r >> 2) & 3));
-            so = 4u * (uint32_t)(n0 + 64 * q + r);
         }
+        const int ntiles = a.tiles_m * a.tiles_n;
+        for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+            const TileIdx ti = tile_of(tile, a.tiles_m, a.tiles_n);
+            const int m0 = ti.tm * 256, n0 = ti.tn * 256;
+            // DMA sources. A: instruction i of wave w fills rows 8 (4 w + i) ..
+            // +7, 8 lanes a row; W: rows 16 (2 w + i) .. +15, 4 lanes a row.
 #pragma unroll
-        for (int i = 0; i < NI; i++)
+            for (int i = 0; i < 4; i++) {
+                const int tr = 8 * (4 * w + i) + (lane >> 3);  // row within the tile
+                const int c = (lane & 7) ^ ((tr >> 1) & 7);
+                const int row = min(m0 + tr, a.M - 1);
+                ga[i] = (uint32_t)row * (uint32_t)a.lda * 2u + 16u * c;
+            }
+            {
+                const int nr = lane >> 2, nc = (lane & 3) ^ ((lane >> 4) & 3);
 #pragma unroll
-            for (int j = 0; j < NJ; j++) acc[i][j] = f32x16{0};
+                for (int i = 0; i < 2; i++)
+                    gb[i] = (uint32_t)(n0 + 16 * (2 * w + i) + nr) * (uint32_t)a.K + 16u * nc;
+            }
+            so = 4u * (uint32_t)(n0 + 64 * q + (lane & 31));
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) acc[i][j] = f32x16{0};
 
-        // scale pairs first: the wait for tile 0 below then covers them too
+            // scale pairs first: the wait for tile 0 below then covers them too
 #pragma unroll
-        for (int j = 0; j < NJ; j++)
-            s2[j] = __builtin_bit_cast(f16x2, __builtin_amdgcn_raw_buffer_load_b32(rs_, so + 128 * j, 0, 0));
-        __builtin_amdgcn_sched_barrier(0);
-        dma<0>(0);
-        dma<1>(1);  // K is a multiple of 128: nk >= 2
-        wait_dma(true);
-        __builtin_amdgcn_s_barrier();
-        if (PP && g == 1) __builtin_amdgcn_s_barrier();
-        // Main loop: three tiles per trip, every one with a DMA two tiles
-        // ahead; the last 2 to 4 tiles follow unrolled.
-        const int trips = (nk - 2) / 3;
-        for (int it = 0; it < trips; it++) {
-            const int k = 3 * it;
-            step<0>(k, true);
-            step<1>(k + 1, true);
-            step<2>(k + 2, true);
+            for (int j = 0; j < NJ; j++)
+                s2[j] = __builtin_bit_cast(f16x2, __builtin_amdgcn_raw_buffer_load_b32(rs_, so + 128 * j, 0, 0));
+            __builtin_amdgcn_sched_barrier(0);
+            dma<0>(0);
+            dma<1>(1);  // K is a multiple of 128: nk >= 2
+            wait_dma(true);
+            __builtin_amdgcn_s_barrier();
+            if (PP && g == 1) __builtin_amdgcn_s_barrier();
+            // Main loop: three tiles per trip, every one with a DMA two tiles
+            // ahead; the last 2 to 4 tiles follow unrolled.
+            const int trips = (nk - 2) / 3;
+            for (int it = 0; it < trips; it++) {
+                const int k = 3 * it;
+                step<0>(k, true);
+                step<1>(k + 1, true);
+                step<2>(k + 2, true);
+            }
+            {
+                const int k = 3 * trips;  // nk - k is 2, 3 or 4
+                step<0>(k, k + 2 < nk);
+                step<1>(k + 1, k + 3 < nk);
+                if (k + 2 < nk) step<2>(k + 2, k + 4 < nk);
+                if (k + 3 < nk) step<0>(k + 3, false);
+            }
+            if (PP && g == 0) __builtin_amdgcn_s_barrier();
+            // Every wave has passed its last barrier: no stage is read or DMA'd
+            // any more, and each wave stages its epilogue in a private 9 KB patch.
+            uint8_t* patch = w < 3 ? q8_sa0 + 9216 * w : w < 6 ? q8_sa1 + 9216 * (w - 3) : q8_sa2 + 9216 * (w - 6);
+            gemm_epilogue_lds<_Float16, EPI, NI, NJ>(a, acc, (float*)patch, m0 + 128 * g, n0 + 64 * q, n0);
+            // every patch has been read back before the next tile's DMA fills
+            // the stages it lives in
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(Q8_WAIT_LGKM0);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
         }
-        {
-            const int k = 3 * trips;  // nk - k is 2, 3 or 4
-            step<0>(k, k + 2 < nk);
-            step<1>(k + 1, k + 3 < nk);
-            if (k + 2 < nk) step<2>(k + 2, k + 4 < nk);
-            if (k + 3 < nk) step<0>(k + 3, false);
-        }
-        if (PP && g == 0) __builtin_amdgcn_s_barrier();
-        // Every wave has passed its last barrier: no stage is read or DMA'd any
-        // more, and each wave stages its epilogue in a private 9 KB patch.
-        uint8_t* patch = w < 3 ? q8_sa0 + 9216 * w : w < 6 ? q8_sa1 + 9216 * (w - 3) : q8_sa2 + 9216 * (w - 6);
-        gemm_epilogue_lds<_Float16, EPI, NI, NJ>(a, acc, (float*)patch, m0 + 128 * g, n0 + 64 * q, n0);
     }
 };
 

@@ -2,6 +2,7 @@
 // as a sequence of gfx950 kernel launches on one stream, plus the isolated
 // operator entry points.
 #include <cmath>
+#include <algorithm>
 #include <cstring>
 
 #include "ltx_internal.hpp"
@@ -148,7 +149,8 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
         std::snprintf(name, sizeof(name), "ltx_gemm_q8_%s%s",
                       epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv",
                       c->gemm_q8 == 2 ? "_pp" : "");
-        c->launch(name, g.tiles_m * g.tiles_n, 1, 1, 512, &g, st, label);
+        const int ntiles = g.tiles_m * g.tiles_n;
+        c->launch(name, c->gemm_persistent ? std::min(ntiles, c->num_cu) : ntiles, 1, 1, 512, &g, st, label);
         return;
     }
     std::snprintf(name, sizeof(name), "ltx_gemm_%s_%s_%s%s", msuffix(mode), bk,

@@ -76,6 +76,8 @@ struct ltx_ctx {
     // waves per workgroup of the register-staged GEMM (4 or 8), attention schedule
     int gemm_q8 = 2;
     int gemm_waves = 8;
+    int num_cu = 256;             // compute units: the persistent GEMM's grid bound
+    bool gemm_persistent = true;  // LDS-DMA GEMM: at most one workgroup per CU, looping over tiles
     // attention: 0: 4 waves x 64 queries, 1: 8 waves x 32, 2: 8 waves, halves phase-shifted,
     // 3: software-pipelined 4 waves x 64 with LDS DMA (whole 32-key tiles; else 1),
     // 4: ping-pong 8 waves x 32 with LDS DMA (whole 64-key tiles; else 1)

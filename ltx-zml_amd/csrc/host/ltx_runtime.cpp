@@ -141,6 +141,10 @@ int ltx_init(int device, ltx_ctx** out) {
             throw ltx::Error(std::string("ltx_init: code objects are gfx950-only, device is ") + prop.gcnArchName);
         c = new ltx_ctx();
         c->device = device;
+        c->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+        // LTX_GEMM_GRID=tile: one workgroup per output tile instead of the
+        // persistent grid of one per CU (A/B timing)
+        if (const char* e = std::getenv("LTX_GEMM_GRID")) c->gemm_persistent = std::strcmp(e, "tile") != 0;
         // variant overrides (used for A/B timing): 4 or 8 waves per workgroup
         if (const char* e = std::getenv("LTX_GEMM_WAVES")) c->gemm_waves = std::atoi(e) == 4 ? 4 : 8;
         if (const char* e = std::getenv("LTX_GEMM_Q8"))
