@@ -666,11 +666,14 @@ extern "C" __global__ void __launch_bounds__(256, 1) ltx_attn_bf16_sp(const LtxA
 // slot c ^ ((d >> 1) & 7). Three stages each, distinct objects.
 //
 // DMA and waits (G0 = waves 0-3 lead, G1 = waves 4-7 follow one phase
-// later): each wave issues K(t+2), V(t+1) at the start of its softmax phase
-// t. G0 then waits for the group it issued one softmax phase earlier at the
-// end of softmax phase t; G1 waits for everything at the end of its MFMA
-// phase t. Either way K(t+1) and V(t) are complete, from both groups, before
-// the barrier after which G0's MFMA phase t+1 reads them.
+// later): G0 issues all of K(t+2) and V(t+1) (its slices and G1's) at the
+// start of its softmax phase t, two phases before its MFMA phase t+2 reads
+// them, and at the end of softmax phase t waits for what it issued one
+// softmax phase earlier: K(t+1) and V(t) are complete before the barrier
+// after which G0's MFMA phase t+1 (and, half a step later, G1's) reads
+// them. G1 issues no DMA: its softmax phase runs one phase after G0's, so
+// slices it issued would have only one phase to land (measured 1 % slower
+// on the whole kernel).
 __shared__ __attribute__((aligned(1024))) uint8_t app_k0[16384];
 __shared__ __attribute__((aligned(1024))) uint8_t app_k1[16384];
 __shared__ __attribute__((aligned(1024))) uint8_t app_k2[16384];
@@ -708,19 +711,30 @@ struct AttnPP {
 
     __device__ __forceinline__ AttnPP(const LtxAttnArgs& args) : a(args) {}
 
+    // Group 0 (waves 0-3) issues every DMA: wave w fills its own 2 KB slice
+    // of a stage and that of wave w + 4 (8 KB further, K rows + 32 = keys
+    // + 32, V^T rows + 64), 4 instructions per K or V tile. Group 0 issues in
+    // its softmax phase t, two phases before its MFMA phase t + 2 needs the
+    // tile (group 1's slices, issued in its own softmax phase, had only one).
     template <int S>
     __device__ __forceinline__ void dma_k(int t) {
         uint8_t* d = app_k<S>() + lw;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (attn_lds_ptr)(d + 1024 * i), 16, gk[i], t * 16384, 0, 0);
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (attn_lds_ptr)(d + 8192 * h + 1024 * i), 16, gk[i],
+                                                         t * 16384 + 8192 * h, 0, 0);
     }
     template <int S>
     __device__ __forceinline__ void dma_v(int t) {
         uint8_t* d = app_v<S>() + lw;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (attn_lds_ptr)(d + 1024 * i), 16, gv[i], t * 128, 0, 0);
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (attn_lds_ptr)(d + 8192 * h + 1024 * i), 16, gv[i],
+                                                         t * 128 + 128 * a.lkv * h, 0, 0);
     }
 
     // MFMA phase t: PV(t-1) from V stage VS, then S(t) from K stage KS
@@ -829,12 +843,13 @@ struct AttnPP {
         mfma_phase<T3, (T3 + 2) % 3>(FULL || t < nt, FULL || t >= 1);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
-        if (g == 1) __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(0));
         barrier();
         if (!FULL && t >= nt) return;
         const bool dk = FULL || t + 2 < nt, dv = FULL || t + 1 < nt;
-        if (dk) dma_k<(T3 + 2) % 3>(t + 2);
-        if (dv) dma_v<(T3 + 1) % 3>(t + 1);
+        if (g == 0) {
+            if (dk) dma_k<(T3 + 2) % 3>(t + 2);
+            if (dv) dma_v<(T3 + 1) % 3>(t + 1);
+        }
         __builtin_amdgcn_sched_barrier(0);
         softmax(!FULL && t == 0);
         // the P^T operands, row sum and bias must exist before the phase ends
@@ -844,11 +859,13 @@ struct AttnPP {
         asm volatile("" ::"v"(l), "v"(m));
         asm volatile("" ::"v"(sb));
         __builtin_amdgcn_sched_barrier(0);
+        // group 0: the previous phase's tiles have landed (this phase's may
+        // still be in flight)
         if (g == 0) {
             if (dk && dv)
-                __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(4));
+                __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(8));
             else if (dk || dv)
-                __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(2));
+                __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(4));
             else
                 __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(0));
         }
@@ -901,11 +918,13 @@ struct AttnPP {
         m = 0.f;
         sb = f32x16{0};
         l = 0.f;
-        // prologue: K(0), K(1), V(0); MFMA phase 0 needs K(0)
-        dma_k<0>(0);
-        dma_k<1>(1);
-        dma_v<0>(0);
-        __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(4));
+        // prologue (group 0): K(0), K(1), V(0); MFMA phase 0 needs K(0)
+        if (g == 0) {
+            dma_k<0>(0);
+            dma_k<1>(1);
+            dma_v<0>(0);
+            __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(8));
+        }
         __builtin_amdgcn_s_barrier();
         if (g == 1) __builtin_amdgcn_s_barrier();  // the second wave of each SIMD starts one phase later
         // steps 0 .. nt (step nt is the PV-only MFMA phase): step 0, a main
