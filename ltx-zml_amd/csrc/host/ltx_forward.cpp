@@ -109,7 +109,7 @@ static void norm_mod(ltx_ctx* c, int mode, const float* x, void* y, LtxAda ada, 
                      hipStream_t st) {
     LtxNormArgs a{x, y, ada, rows, ish, isc};
     const char* k = mode == LTX_MODE_F32 ? "ltx_norm_mod_f32" : mode == LTX_MODE_BF16 ? "ltx_norm_mod_bf16" : "ltx_norm_mod_f16";
-    c->launch(k, rows, 1, 1, 256, &a, st);
+    c->launch(k, (rows + 3) / 4, 1, 1, 256, &a, st);  // four rows per workgroup (NORM_ROWS)
 }
 
 // 16-bit GEMM: y = A . W^T with the given epilogue.

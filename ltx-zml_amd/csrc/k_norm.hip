@@ -1,58 +1,76 @@
 // Bandwidth-bound kernels: fused RMSNorm + AdaLN modulate, the cross-attention
 // K/V modulation, and the full-row qk RMSNorm + split-half 3D RoPE.
-// One 256-thread workgroup per token row of D = 4096 channels.
+// 256-thread workgroups over token rows of D = 4096 channels.
 #include "ltx_device.h"
 
 // RMSNorm + modulate (ltx/block.zig:28-30, 36-38, 248-252, 548-552, 569-572):
 // y = x * rsqrt(mean(x^2) + 1e-6) * (1 + ada[isc]) + ada[ish].
-// Each thread owns 4 float4 columns c = 4*tid + 1024*i.
+// Each thread owns 4 float4 columns c = 4*tid + 1024*i. A workgroup takes
+// NORM_ROWS consecutive rows; when their timestep rows agree (the usual case:
+// runs of tokens share one), the scale and shift rows (tstab + sst) are
+// formed once for all of them, which quarters their L2 reads (64 KB per row
+// otherwise, four times the row's own bytes).
+#define NORM_ROWS 4
 template <int OUT>  // 0: f16, 1: bf16, 2: f32
 __device__ void norm_mod_body(const LtxNormArgs& a) {
     __shared__ float red[4];
-    int row = blockIdx.x;
-    if (row >= a.rows) return;
-    const float4* x = (const float4*)(a.x + (size_t)row * LTX_D);
-    float4 v[4];
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) v[i] = x[threadIdx.x + 256 * i];
-    // the modulation rows do not depend on the row statistics: loaded before
-    // the reduction so their latency overlaps it
-    float4 sct[4], scs[4], sht[4], shs[4];
-    if (a.isc >= 0) {
-        const int r = a.ada.tidx[row];
+    const int row0 = blockIdx.x * NORM_ROWS;
+    if (row0 >= a.rows) return;
+    const int nr = min(NORM_ROWS, a.rows - row0);
+    const bool mod = a.isc >= 0;
+    bool shared_mod = mod;
+    if (mod) {
+        const int r0 = a.ada.tidx[row0];
+        for (int k = 1; k < nr; k++) shared_mod = shared_mod && a.ada.tidx[row0 + k] == r0;
+    }
+    float4 sc1[4], sh[4];  // 1 + scale, shift
+    auto load_mod = [&](int r) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int c = 4 * (threadIdx.x + 256 * i);
-            sct[i] = *(const float4*)(a.ada.tstab + ((size_t)r * 9 + a.isc) * LTX_D + c);
-            scs[i] = *(const float4*)(a.ada.sst + (size_t)a.isc * LTX_D + c);
-            sht[i] = *(const float4*)(a.ada.tstab + ((size_t)r * 9 + a.ish) * LTX_D + c);
-            shs[i] = *(const float4*)(a.ada.sst + (size_t)a.ish * LTX_D + c);
+            const float4 sct = *(const float4*)(a.ada.tstab + ((size_t)r * 9 + a.isc) * LTX_D + c);
+            const float4 scs = *(const float4*)(a.ada.sst + (size_t)a.isc * LTX_D + c);
+            const float4 sht = *(const float4*)(a.ada.tstab + ((size_t)r * 9 + a.ish) * LTX_D + c);
+            const float4 shs = *(const float4*)(a.ada.sst + (size_t)a.ish * LTX_D + c);
+            sc1[i] = make_float4((sct.x + scs.x) + 1.0f, (sct.y + scs.y) + 1.0f, (sct.z + scs.z) + 1.0f,
+                                 (sct.w + scs.w) + 1.0f);
+            sh[i] = make_float4(sht.x + shs.x, sht.y + shs.y, sht.z + shs.z, sht.w + shs.w);
         }
-    }
+    };
+    if (shared_mod) load_mod(a.ada.tidx[row0]);
+    for (int k = 0; k < nr; k++) {
+        const int row = row0 + k;
+        const float4* x = (const float4*)(a.x + (size_t)row * LTX_D);
+        float4 v[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
-    ss = block_sum256(ss, red);
-    float inv = 1.0f / sqrtf(ss * (1.0f / LTX_D) + 1e-6f);
+        for (int i = 0; i < 4; i++) v[i] = x[threadIdx.x + 256 * i];
+        // rows with their own timestep row: its modulation rows load before
+        // the reduction so their latency overlaps it
+        if (mod && !shared_mod) load_mod(a.ada.tidx[row]);
+        float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        int c = 4 * (threadIdx.x + 256 * i);
-        float o[4] = {v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv};
-        if (a.isc >= 0) {
-            float sc[4] = {sct[i].x + scs[i].x, sct[i].y + scs[i].y, sct[i].z + scs[i].z, sct[i].w + scs[i].w};
-            float sh[4] = {sht[i].x + shs[i].x, sht[i].y + shs[i].y, sht[i].z + shs[i].z, sht[i].w + shs[i].w};
+        for (int i = 0; i < 4; i++) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+        ss = block_sum256(ss, red);
+        const float inv = 1.0f / sqrtf(ss * (1.0f / LTX_D) + 1e-6f);
 #pragma unroll
-            for (int j = 0; j < 4; j++) o[j] = o[j] * (sc[j] + 1.0f) + sh[j];
-        }
-        size_t off = (size_t)row * LTX_D + c;
-        if (OUT == 2) {
-            *(float4*)((float*)a.y + off) = make_float4(o[0], o[1], o[2], o[3]);
-        } else if (OUT == 0) {
-            u32x2 p = {pack2<_Float16>(o[0], o[1]), pack2<_Float16>(o[2], o[3])};
-            *(u32x2*)((uint16_t*)a.y + off) = p;
-        } else {
-            u32x2 p = {pack2<__bf16>(o[0], o[1]), pack2<__bf16>(o[2], o[3])};
-            *(u32x2*)((uint16_t*)a.y + off) = p;
+        for (int i = 0; i < 4; i++) {
+            const int c = 4 * (threadIdx.x + 256 * i);
+            float o[4] = {v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv};
+            if (mod) {
+                const float s1[4] = {sc1[i].x, sc1[i].y, sc1[i].z, sc1[i].w}, s0[4] = {sh[i].x, sh[i].y, sh[i].z, sh[i].w};
+#pragma unroll
+                for (int j = 0; j < 4; j++) o[j] = o[j] * s1[j] + s0[j];
+            }
+            const size_t off = (size_t)row * LTX_D + c;
+            if (OUT == 2) {
+                *(float4*)((float*)a.y + off) = make_float4(o[0], o[1], o[2], o[3]);
+            } else if (OUT == 0) {
+                u32x2 p = {pack2<_Float16>(o[0], o[1]), pack2<_Float16>(o[2], o[3])};
+                *(u32x2*)((uint16_t*)a.y + off) = p;
+            } else {
+                u32x2 p = {pack2<__bf16>(o[0], o[1]), pack2<__bf16>(o[2], o[3])};
+                *(u32x2*)((uint16_t*)a.y + off) = p;
+            }
         }
     }
 }
