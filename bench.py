@@ -31,7 +31,7 @@ PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
 # HBM bytes per self-attention launch from rocprofv3 FETCH_SIZE (x2.0, the
 # factor a 1 GiB copy calibrates) + WRITE_SIZE (x1.0), for the kernel as
 # built at that measurement (profiles/attn_self_t28672_f16_hbm_bytes.md).
-ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.468e9}
+ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.474e9}
 
 
 def flops(T: int, S: int) -> dict:
