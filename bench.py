@@ -58,7 +58,7 @@ def cpu_baseline(T: int, S: int, threads: int) -> dict:
     rng = np.random.default_rng(0)
     w = bf.bf16_bits((rng.standard_normal((FF, D)) * 0.02).astype(np.float32))
     q, s = bf.quantize_g128(w)
-    m1, m2 = 512, 1536
+    m1, m2 = 2048, 8192
     xs = rng.standard_normal((m2, D)).astype(np.float32)
     oracle.linear(xs[:64], q=q, s=s, real="f32")  # warm
     t0 = time.perf_counter()
@@ -68,7 +68,7 @@ def cpu_baseline(T: int, S: int, threads: int) -> dict:
     t2 = time.perf_counter()
     rate = 2.0 * (m2 - m1) * FF * D / max((t2 - t1) - (t1 - t0), 1e-9)
     prep_per_param = max((t1 - t0) - 2.0 * m1 * FF * D / rate, 0.0) / (FF * D)
-    lq = 64
+    lq = 1024
     qa = rng.standard_normal((lq, D)).astype(np.float32)
     ka = rng.standard_normal((T, D)).astype(np.float32)
     va = rng.standard_normal((T, D)).astype(np.float32)
