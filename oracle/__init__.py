@@ -135,6 +135,12 @@ def block_forward(bt, inp: dict, cos_thf: np.ndarray, sin_thf: np.ndarray, chunk
     q8s = (C.c_void_p * 10)(*[bt.q8s[n].ctypes.data if n in bt.q8s else None for n in Q_ORDER])
     x = np.ascontiguousarray(inp["x"], np.float32)
     T, S = x.shape[0], inp["ctx"].shape[0]
+    # the blockwise attention's chunk must divide the key count
+    # (ltx/block.zig:112); the C code would return NaN rows
+    if chunk > 0 and T % chunk:
+        raise ValueError(f"chunk {chunk} does not divide the token count {T}")
+    if cross_chunk > 0 and S % cross_chunk:
+        raise ValueError(f"cross_chunk {cross_chunk} does not divide the context length {S}")
     out = np.empty((T, D), dt)
     st_bufs = {}
     st_arr = None

@@ -190,3 +190,20 @@ def test_block_zero_gates_identity(small_case):
     bt2 = bf.BlockTensors(0, base, bt.q8, bt.q8s)
     out = oracle.block_forward(bt2, inp, cos, sin, chunk=16)
     assert np.array_equal(out, inp["x"].astype(np.float64))
+
+
+def test_block_chunk_must_divide_keys(block0):
+    """The blockwise attention's chunk must divide the key count, as the
+    reference asserts (ltx/block.zig:112); the dense softmax (chunk 0) takes
+    any length and agrees with a dividing chunk."""
+    inp = synth.make_inputs(20, 8, sigma=0.7)
+    c, s = oracle.rope_tables(inp["grid"])
+    c, s = np.ascontiguousarray(c.transpose(1, 0, 2)), np.ascontiguousarray(s.transpose(1, 0, 2))
+    with pytest.raises(ValueError):
+        oracle.block_forward(block0, inp, c, s, chunk=16)
+    with pytest.raises(ValueError):
+        oracle.block_forward(block0, inp, c, s, chunk=10, cross_chunk=3)
+    dense = oracle.block_forward(block0, inp, c, s, chunk=0)
+    blk = oracle.block_forward(block0, inp, c, s, chunk=10, cross_chunk=4)
+    assert np.isfinite(dense).all()
+    assert oracle.rel_rms(blk, dense) < 1e-12
