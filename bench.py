@@ -156,6 +156,85 @@ def denoise_bench(args) -> int:
     return 0
 
 
+GEMM_SWEEP = [(4096, 4096, 4096), (28672, 4096, 4096), (28672, 4096, 16384), (28672, 16384, 4096)]  # M, K, N
+ATTN_SWEEP = [(4096, 4096), (16384, 16384), (28672, 28672), (28672, 256)]  # Lq, Lkv
+
+
+def sweep_bench(args) -> int:
+    """The isolated kernels through the C ABI (ltx_op_linear_q8,
+    ltx_op_attention) at the reference's microbenchmark shapes
+    (ltx/smoke.zig): the W8A16 GEMM (A N(0, 1), W Student-t(3) x 0.02 int8
+    grouped-128 with fp16 scales, 16-bit output, f32 accumulate) and
+    non-causal attention (32 heads x 128, Q/K/V N(0, 1), scale 1/sqrt(128),
+    f32 softmax statistics). Kernel time from HIP events around each launch
+    (the op's one-off weight preparation is not in it). Prints one JSON line."""
+    import numpy as np
+    import torch
+
+    from ltx_amd import blockfmt as bf
+    from ltx_amd import runtime as rt
+
+    ctx = rt.Context(0)
+    modes = ["f16", "bf16"] if args.mode == "f16" else [args.mode]
+    reps = max(args.steps, 1)
+    rows = []
+
+    def timed(fn, substr):
+        for _ in range(max(args.warmup, 1)):
+            fn()
+        torch.cuda.synchronize()
+        ctx.profile(True)
+        ctx.profile_reset()
+        for _ in range(reps):
+            fn()
+        tot, n = ctx.profile_read(substr)
+        ctx.profile(False)
+        return tot / max(n, 1)
+
+    for M, K, N in GEMM_SWEEP:
+        g = np.random.default_rng(M + 3 * K + 7 * N)
+        q, s = bf.quantize_g128(bf.bf16_bits((g.standard_t(3, size=(N, K)) * 0.02).astype(np.float32)))
+        dq, ds = torch.from_numpy(q).cuda(), torch.from_numpy(s.astype(np.float16)).cuda()
+        del q, s
+        for mode in modes:
+            dt = torch.float16 if mode == "f16" else torch.bfloat16
+            a = torch.randn((M, K), dtype=dt, device="cuda")
+            y = torch.empty((M, N), dtype=dt, device="cuda")
+            ms = timed(lambda: ctx.linear_q8(a, dq, ds, None, y, mode=rt.MODES[mode]), "ltx_gemm")
+            assert torch.isfinite(y).all().item(), "non-finite GEMM output"
+            tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+            log(f"bench: gemm {M}x{K}x{N} {mode}: {ms:.3f} ms, {tf:.0f} TFLOP/s")
+            rows.append({"kernel": "gemm", "M": M, "K": K, "N": N, "dtype": mode, "ms": round(ms, 4),
+                         "tflops": round(tf, 1), "frac": round(tf / PEAK_TFLOPS, 4)})
+            del a, y
+        del dq, ds
+        torch.cuda.empty_cache()
+    for lq, lkv in ATTN_SWEEP:
+        for mode in modes:
+            dt = torch.float16 if mode == "f16" else torch.bfloat16
+            q = torch.randn((H, lq, HD), dtype=dt, device="cuda")
+            k = torch.randn((H, lkv, HD), dtype=dt, device="cuda")
+            vt = torch.randn((H, HD, lkv), dtype=dt, device="cuda")
+            out = torch.empty((lq, D), dtype=dt, device="cuda")
+            ms = timed(lambda: ctx.attention(q, k, vt, None, out, lq, lkv, mode=rt.MODES[mode]), "ltx_attn")
+            assert torch.isfinite(out).all().item(), "non-finite attention output"
+            tf = 4.0 * H * lq * lkv * HD / (ms * 1e-3) / 1e12
+            log(f"bench: attention {lq}x{lkv} {mode}: {ms:.3f} ms, {tf:.0f} TFLOP/s")
+            rows.append({"kernel": "attention", "Lq": lq, "Lkv": lkv, "dtype": mode, "ms": round(ms, 4),
+                         "tflops": round(tf, 1), "frac": round(tf / PEAK_TFLOPS, 4)})
+            del q, k, vt, out
+    ctx.close()
+    best = max(r["tflops"] for r in rows if r["kernel"] == "attention" and r["Lq"] == r["Lkv"] == 28672)
+    print(json.dumps({
+        "metric": "isolated W8A16 GEMM and attention kernels, TFLOP/s", "value": best, "unit": "TFLOP/s",
+        "higher_is_better": True, "n_gpus": 1, "steps": reps, "warmup": args.warmup, "data": "synthetic",
+        "peak_tflops": PEAK_TFLOPS,
+        "config": {"workload": "GEMM M x K x N and attention Lq x Lkv sweep, 32 heads x 128",
+                   "value_is": "self-attention at L = 28,672"},
+        "results": rows}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -168,6 +247,9 @@ def main() -> int:
     ap.add_argument("--denoise", type=int, default=0, metavar="BLOCKS",
                     help="instead of the block line: time the stage-1 denoising loop (8 Euler steps) over this "
                          "many resident blocks (48 for the whole transformer) and print its own JSON line")
+    ap.add_argument("--sweep", action="store_true",
+                    help="instead of the block line: time the isolated GEMM and attention kernels at the "
+                         "microbenchmark shapes (f16 and bf16 operands) and print their own JSON line")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="run one plain device-to-device copy of this many MiB before the timed steps "
                          "(the known-size kernel that calibrates HBM byte counters)")
@@ -186,6 +268,8 @@ def main() -> int:
     T, S = args.tokens, args.text
     if args.denoise:
         return denoise_bench(args)
+    if args.sweep:
+        return sweep_bench(args)
     t0 = time.time()
     bt = synth.make_block(0, seed=1, dist="t3", classes=("qkv", "ff", "out"), scale_dtype="F16")
     inp = synth.make_inputs(T, S, sigma=0.7)
