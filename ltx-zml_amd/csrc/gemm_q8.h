@@ -1,12 +1,12 @@
 // W8A16 GEMM for gfx950 with LDS-DMA staging: y[M][N] = A[M][K] . W[N][K]^T,
-// A f16 activations, W int8 with one f16 scale per 128 consecutive k
+// A f16 (or bf16) activations, W int8 with one f16 scale per 128 consecutive k
 // (ltx/block.zig:462-471), fused epilogues as in gemm_common.h. The scales
 // arrive as pairs: a.scales is u32 [K / 128][N], each word the f16 scale in
 // both halves (laid out once at upload).
 //
 // Workgroup: 8 waves (two per SIMD), output tile 256 x 256; wave w owns rows
 // 128 (w / 4) .. +127 and columns 64 (w % 4) .. +63 (4 x 2 blocks of 32 x 32,
-// v_mfma_f32_32x32x16_f16, f32 accumulate).
+// v_mfma_f32_32x32x16_f16 or _bf16, f32 accumulate).
 //
 // K is walked in tiles of 64. Each tile's A (256 x 64 f16, 32 KB) and W
 // (256 x 64 int8, 16 KB) go straight from global memory into LDS with
@@ -19,7 +19,10 @@
 // 0x80, done once at upload), the f16 with bits 0x6400 | u is 1024 + u;
 // subtracting 1152 gives q exactly and one f16 multiply by the f16 scale
 // rounds q * s once to nearest even — the operand RNE16(q * s) that the
-// register-staged kernels also feed the MFMA.
+// register-staged kernels also feed the MFMA. For bf16 operands (no packed
+// bf16 multiply on gfx950) each byte u goes to f32 exactly (v_cvt_f32_ubyteN)
+// and fma(u, s, -128 s) is q * s exactly (at most 19 significant bits), then
+// one v_cvt_pk_bf16_f32 rounds a pair to nearest even: RNE_bf16(q * s).
 //
 // LDS layout: A rows of 128 B (8 chunks of 8 k), chunk c of row r stored in
 // slot c ^ ((r >> 1) & 7) (16 consecutive rows, one ds_read_b128 lane group,
@@ -80,11 +83,60 @@ __device__ __forceinline__ f16x8 q8_dequant8(uint32_t w0, uint32_t w1, f16x2 s2)
     return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
 }
 
+// The operand type's part of the kernel: the scale form a lane keeps for one
+// column (from its scale-pair word), the dequantisation of 8 weights and the
+// MFMA.
+template <typename T>
+struct Q8Op;
+
+template <>
+struct Q8Op<_Float16> {
+    typedef f16x2 Scale;  // the f16 scale in both halves
+    typedef f16x8 V8;
+    static __device__ __forceinline__ Scale scale(uint32_t pair) { return __builtin_bit_cast(f16x2, pair); }
+    static __device__ __forceinline__ V8 deq8(uint32_t w0, uint32_t w1, Scale s) { return q8_dequant8(w0, w1, s); }
+    static __device__ __forceinline__ f32x16 mfma(u32x4 a, V8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), b, c, 0, 0, 0);
+    }
+};
+
+struct Q8ScaleF32 {
+    float s, c;  // the scale and -128 times it, both exact in f32
+};
+
+template <>
+struct Q8Op<__bf16> {
+    typedef Q8ScaleF32 Scale;
+    typedef bf16x8 V8;
+    static __device__ __forceinline__ Scale scale(uint32_t pair) {
+        const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)(pair & 0xffffu));
+        return Scale{s, -128.0f * s};
+    }
+    static __device__ __forceinline__ V8 deq8(uint32_t w0, uint32_t w1, Scale s) {
+        uint32_t o[4];
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+            const uint32_t x = d ? w1 : w0;
+            const float f0 = __builtin_fmaf((float)(x & 0xffu), s.s, s.c);
+            const float f1 = __builtin_fmaf((float)((x >> 8) & 0xffu), s.s, s.c);
+            const float f2 = __builtin_fmaf((float)((x >> 16) & 0xffu), s.s, s.c);
+            const float f3 = __builtin_fmaf((float)(x >> 24), s.s, s.c);
+            o[2 * d] = Op<__bf16>::cvt2(f0, f1);
+            o[2 * d + 1] = Op<__bf16>::cvt2(f2, f3);
+        }
+        return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
+    }
+    static __device__ __forceinline__ f32x16 mfma(u32x4 a, V8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
+    }
+};
+
 // Raw buffer descriptor word 3 for gfx9-family parts (untyped dword access).
 #define Q8_RSRC_W3 0x00020000
 
-template <int EPI, bool PP>
+template <typename T, int EPI, bool PP>
 struct Q8Gemm {
+    typedef Q8Op<T> QO;
     static constexpr int NI = 4, NJ = 2;
     const LtxGemmArgs& a;
     f32x16 acc[NI][NJ];
@@ -94,7 +146,7 @@ struct Q8Gemm {
     int la, lb;             // this wave's DMA destinations within a stage (uniform)
     uint32_t offa[4], offb[2];
     uint32_t so;            // byte offset of the lane's first scale pair in group 0
-    f16x2 s2[NJ];
+    typename QO::Scale s2[NJ];
 
     __device__ __forceinline__ Q8Gemm(const LtxGemmArgs& args) : a(args) {}
 
@@ -144,7 +196,7 @@ struct Q8Gemm {
         // ping-pong: the first DQ k-steps are dequantised in this (memory)
         // phase, so the MFMA phase opens with MFMAs; the rest interleave with it
         constexpr int DQ = PP ? 2 : 0;
-        f16x8 fb0[DQ > 0 ? DQ : 1][NJ];
+        typename QO::V8 fb0[DQ > 0 ? DQ : 1][NJ];
         if (PP) {
             __builtin_amdgcn_s_waitcnt(Q8_WAIT_LGKM0);
 #pragma unroll
@@ -152,7 +204,7 @@ struct Q8Gemm {
 #pragma unroll
                 for (int j = 0; j < NJ; j++) {
                     const u32x4 w = wb[j][t >> 1];
-                    fb0[t][j] = (t & 1) ? q8_dequant8(w[2], w[3], s2[j]) : q8_dequant8(w[0], w[1], s2[j]);
+                    fb0[t][j] = (t & 1) ? QO::deq8(w[2], w[3], s2[j]) : QO::deq8(w[0], w[1], s2[j]);
                 }
             if (g == 1) wait_dma(more2);
             __builtin_amdgcn_sched_barrier(0);
@@ -164,21 +216,20 @@ struct Q8Gemm {
         }
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            f16x8 fb[NJ];
+            typename QO::V8 fb[NJ];
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
                 const u32x4 w = wb[j][t >> 1];
                 if (t < DQ)
                     fb[j] = fb0[t < DQ ? t : 0][j];
                 else
-                    fb[j] = (t & 1) ? q8_dequant8(w[2], w[3], s2[j]) : q8_dequant8(w[0], w[1], s2[j]);
+                    fb[j] = (t & 1) ? QO::deq8(w[2], w[3], s2[j]) : QO::deq8(w[0], w[1], s2[j]);
             }
 #pragma unroll
             for (int i = 0; i < NI; i++)
 #pragma unroll
                 for (int j = 0; j < NJ; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, fa[i][t]), fb[j],
-                                                                        acc[i][j], 0, 0, 0);
+                    acc[i][j] = QO::mfma(fa[i][t], fb[j], acc[i][j]);
         }
         __builtin_amdgcn_sched_barrier(0);
         if (PP) __builtin_amdgcn_s_setprio(0);
@@ -187,7 +238,7 @@ struct Q8Gemm {
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < NJ; j++) s2[j] = __builtin_bit_cast(f16x2, sn[j]);
+        for (int j = 0; j < NJ; j++) s2[j] = QO::scale(sn[j]);
     }
 
     // One output tile per trip of a persistent loop: the grid is at most one
@@ -244,7 +295,7 @@ struct Q8Gemm {
             // scale pairs first: the wait for tile 0 below then covers them too
 #pragma unroll
             for (int j = 0; j < NJ; j++)
-                s2[j] = __builtin_bit_cast(f16x2, __builtin_amdgcn_raw_buffer_load_b32(rs_, so + 128 * j, 0, 0));
+                s2[j] = QO::scale(__builtin_amdgcn_raw_buffer_load_b32(rs_, so + 128 * j, 0, 0));
             __builtin_amdgcn_sched_barrier(0);
             dma<0>(0);
             dma<1>(1);  // K is a multiple of 128: nk >= 2
@@ -271,7 +322,7 @@ struct Q8Gemm {
             // Every wave has passed its last barrier: no stage is read or DMA'd
             // any more, and each wave stages its epilogue in a private 9 KB patch.
             uint8_t* patch = w < 3 ? q8_sa0 + 9216 * w : w < 6 ? q8_sa1 + 9216 * (w - 3) : q8_sa2 + 9216 * (w - 6);
-            gemm_epilogue_lds<_Float16, EPI, NI, NJ>(a, acc, (float*)patch, m0 + 128 * g, n0 + 64 * q, n0);
+            gemm_epilogue_lds<T, EPI, NI, NJ>(a, acc, (float*)patch, m0 + 128 * g, n0 + 64 * q, n0);
             // every patch has been read back before the next tile's DMA fills
             // the stages it lives in
             __builtin_amdgcn_sched_barrier(0);
@@ -282,12 +333,12 @@ struct Q8Gemm {
     }
 };
 
-#define Q8_GEMM_KERNEL(NAME, EPI_)                                                           \
+#define Q8_GEMM_KERNEL(NAME, T_, EPI_)                                                       \
     extern "C" __global__ void __launch_bounds__(512, 1) NAME(const LtxGemmArgs a) {         \
-        Q8Gemm<EPI_, false> k(a);                                                            \
+        Q8Gemm<T_, EPI_, false> k(a);                                                        \
         k.run();                                                                             \
     }                                                                                        \
     extern "C" __global__ void __launch_bounds__(512, 1) NAME##_pp(const LtxGemmArgs a) {    \
-        Q8Gemm<EPI_, true> k(a);                                                             \
+        Q8Gemm<T_, EPI_, true> k(a);                                                         \
         k.run();                                                                             \
     }

@@ -107,7 +107,7 @@ def test_linear_q8(ctx, mode, M, N, K, gelu, out_f32, scale_f16):
     assert oracle.rel_rms(got, exact_w) <= (1e-3 if mode == "f16" else 6e-3)
 
 
-def _onehot_case(ctx, M, N, K, seed):
+def _onehot_case(ctx, M, N, K, seed, mode="f16"):
     """y = E . W^T with E[m][k] = (k == m mod K): every output is one weight
     operand times 1, so y must equal the 16-bit operand RNE16(q * s) bit for
     bit (one nonzero product, f32 accumulation)."""
@@ -118,17 +118,23 @@ def _onehot_case(ctx, M, N, K, seed):
     e[np.arange(M), np.arange(M) % K] = 1.0
     dq, ds = torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda()
     y = torch.empty((M, N), dtype=torch.float32, device="cuda")
-    ctx.linear_q8(to16(e, torch.float16).cuda(), dq, ds, None, y, mode=rt.MODE_F16)
+    m, dt = MODES[mode]
+    ctx.linear_q8(to16(e, dt).cuda(), dq, ds, None, y, mode=m)
     torch.cuda.synchronize()
-    exact = q.astype(np.float64) * np.repeat(s.astype(np.float64), 128, axis=1)
-    want = exact.astype(np.float16).astype(np.float32)[:, np.arange(M) % K].T
+    exact = q.astype(np.float64) * np.repeat(s.astype(np.float64), 128, axis=1)  # exact in f32 too
+    if mode == "f16":
+        op = exact.astype(np.float16).astype(np.float32)
+    else:
+        op = bf.bf16_to_f32(bf.bf16_bits(exact.astype(np.float32)))
+    want = op[:, np.arange(M) % K].T
     return y.cpu().numpy(), want
 
 
+@pytest.mark.parametrize("mode", ["f16", "bf16"])
 @pytest.mark.parametrize("M,N,K", [(1024, 512, 1024), (300, 256, 256)])
-def test_linear_q8_onehot_exact(ctx, M, N, K):
-    say(f"linear_q8 one-hot f16 M={M} N={N} K={K}")
-    got, want = _onehot_case(ctx, M, N, K, seed=M + K)
+def test_linear_q8_onehot_exact(ctx, M, N, K, mode):
+    say(f"linear_q8 one-hot {mode} M={M} N={N} K={K}")
+    got, want = _onehot_case(ctx, M, N, K, seed=M + K, mode=mode)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
@@ -140,8 +146,9 @@ def test_linear_q8_variants(monkeypatch, variant):
     monkeypatch.setenv("LTX_GEMM_Q8", variant)
     c = rt.Context(0)
     try:
-        got, want = _onehot_case(c, 1024, 512, 1024, seed=9)
-        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        for mode in ("f16", "bf16"):
+            got, want = _onehot_case(c, 1024, 512, 1024, seed=9, mode=mode)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), mode
         a, q, s, b = _gemm_case(300, 768, 4096, seed=11, scale_f16=True)
         y = torch.empty((300, 768), dtype=torch.float32, device="cuda")
         c.linear_q8(to16(a, torch.float16).cuda(), torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(),
