@@ -164,7 +164,8 @@ def sweep_bench(args) -> int:
     """The isolated kernels through the C ABI (ltx_op_linear_q8,
     ltx_op_attention) at the reference's microbenchmark shapes
     (ltx/smoke.zig): the W8A16 GEMM (A N(0, 1), W Student-t(3) x 0.02 int8
-    grouped-128 with fp16 scales, 16-bit output, f32 accumulate) and
+    grouped-128 with fp16 scales, and with f32 scales in the first operand
+    type, 16-bit output, f32 accumulate) and
     non-causal attention (32 heads x 128, Q/K/V N(0, 1), scale 1/sqrt(128),
     f32 softmax statistics). Kernel time from HIP events around each launch
     (the op's one-off weight preparation is not in it). Prints one JSON line."""
@@ -194,20 +195,23 @@ def sweep_bench(args) -> int:
     for M, K, N in GEMM_SWEEP:
         g = np.random.default_rng(M + 3 * K + 7 * N)
         q, s = bf.quantize_g128(bf.bf16_bits((g.standard_t(3, size=(N, K)) * 0.02).astype(np.float32)))
-        dq, ds = torch.from_numpy(q).cuda(), torch.from_numpy(s.astype(np.float16)).cuda()
+        dq = torch.from_numpy(q).cuda()
+        scales = {"f16": torch.from_numpy(s.astype(np.float16)).cuda(), "f32": torch.from_numpy(s).cuda()}
         del q, s
-        for mode in modes:
+        # fp16 scales in each operand type, and the f32 scales of the reference's own format
+        for mode, sdt in [(m, "f16") for m in modes] + [(modes[0], "f32")]:
             dt = torch.float16 if mode == "f16" else torch.bfloat16
+            ds = scales[sdt]
             a = torch.randn((M, K), dtype=dt, device="cuda")
             y = torch.empty((M, N), dtype=dt, device="cuda")
             ms = timed(lambda: ctx.linear_q8(a, dq, ds, None, y, mode=rt.MODES[mode]), "ltx_gemm")
             assert torch.isfinite(y).all().item(), "non-finite GEMM output"
             tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-            log(f"bench: gemm {M}x{K}x{N} {mode}: {ms:.3f} ms, {tf:.0f} TFLOP/s")
-            rows.append({"kernel": "gemm", "M": M, "K": K, "N": N, "dtype": mode, "ms": round(ms, 4),
+            log(f"bench: gemm {M}x{K}x{N} {mode} {sdt} scales: {ms:.3f} ms, {tf:.0f} TFLOP/s")
+            rows.append({"kernel": "gemm", "M": M, "K": K, "N": N, "dtype": mode, "scales": sdt, "ms": round(ms, 4),
                          "tflops": round(tf, 1), "frac": round(tf / PEAK_TFLOPS, 4)})
             del a, y
-        del dq, ds
+        del dq, scales
         torch.cuda.empty_cache()
     for lq, lkv in ATTN_SWEEP:
         for mode in modes:

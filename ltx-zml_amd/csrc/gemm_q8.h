@@ -1,8 +1,8 @@
 // W8A16 GEMM for gfx950 with LDS-DMA staging: y[M][N] = A[M][K] . W[N][K]^T,
-// A f16 (or bf16) activations, W int8 with one f16 scale per 128 consecutive k
-// (ltx/block.zig:462-471), fused epilogues as in gemm_common.h. The scales
-// arrive as pairs: a.scales is u32 [K / 128][N], each word the f16 scale in
-// both halves (laid out once at upload).
+// A f16 (or bf16) activations, W int8 with one f16 (or f32) scale per 128
+// consecutive k (ltx/block.zig:462-471), fused epilogues as in gemm_common.h.
+// The scales arrive as words: a.scales is u32 [K / 128][N], each word an f16
+// scale in both halves or an f32 scale's bits (laid out once at upload).
 //
 // Workgroup: 8 waves (two per SIMD), output tile 256 x 256; wave w owns rows
 // 128 (w / 4) .. +127 and columns 64 (w % 4) .. +63 (4 x 2 blocks of 32 x 32,
@@ -20,9 +20,12 @@
 // subtracting 1152 gives q exactly and one f16 multiply by the f16 scale
 // rounds q * s once to nearest even — the operand RNE16(q * s) that the
 // register-staged kernels also feed the MFMA. For bf16 operands (no packed
-// bf16 multiply on gfx950) each byte u goes to f32 exactly (v_cvt_f32_ubyteN)
-// and fma(u, s, -128 s) is q * s exactly (at most 19 significant bits), then
-// one v_cvt_pk_bf16_f32 rounds a pair to nearest even: RNE_bf16(q * s).
+// bf16 multiply on gfx950) and for f32 scales, each byte u goes to f32
+// exactly (v_cvt_f32_ubyteN) and the staging arithmetic of the
+// register-staged kernels follows: f16 operands take one rounding of the
+// exact fma(u, s, -128 s) = q * s (v_fma_mix), bf16 operands the RNE of its
+// f32 value f32(q) * s, the reference's dequantised weight. With f16 scales
+// q * s is exact in f32 (at most 19 significant bits) and the two agree.
 //
 // LDS layout: A rows of 128 B (8 chunks of 8 k), chunk c of row r stored in
 // slot c ^ ((r >> 1) & 7) (16 consecutive rows, one ds_read_b128 lane group,
@@ -83,60 +86,95 @@ __device__ __forceinline__ f16x8 q8_dequant8(uint32_t w0, uint32_t w1, f16x2 s2)
     return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
 }
 
-// The operand type's part of the kernel: the scale form a lane keeps for one
-// column (from its scale-pair word), the dequantisation of 8 weights and the
-// MFMA.
-template <typename T>
+// The operand type's and scale type's part of the kernel: the scale form a
+// lane keeps for one column (from its scale word), the dequantisation of 8
+// weights and the MFMA.
+template <typename T, bool SF32>
 struct Q8Op;
 
+template <typename T>
+struct Q8Mfma;
 template <>
-struct Q8Op<_Float16> {
-    typedef f16x2 Scale;  // the f16 scale in both halves
+struct Q8Mfma<_Float16> {
     typedef f16x8 V8;
-    static __device__ __forceinline__ Scale scale(uint32_t pair) { return __builtin_bit_cast(f16x2, pair); }
-    static __device__ __forceinline__ V8 deq8(uint32_t w0, uint32_t w1, Scale s) { return q8_dequant8(w0, w1, s); }
     static __device__ __forceinline__ f32x16 mfma(u32x4 a, V8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), b, c, 0, 0, 0);
     }
 };
+template <>
+struct Q8Mfma<__bf16> {
+    typedef bf16x8 V8;
+    static __device__ __forceinline__ f32x16 mfma(u32x4 a, V8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
+    }
+};
 
 struct Q8ScaleF32 {
-    float s, c;  // the scale and -128 times it, both exact in f32
+    float s, c;  // the scale and -128 times it (exact: a power of two)
+};
+
+// 8 weights through fma(u, s, -128 s), the staging arithmetic of the
+// register-staged kernels and the dequant probe (deq_pack2): for f16 one
+// rounding of the exact q * s (v_fma_mix), for bf16 RNE of the f32 value.
+__device__ __forceinline__ uint32_t q8_pair_f32(const _Float16*, float u0, float u1, Q8ScaleF32 s) {
+    return deq_pack2<_Float16>(u0, u1, s.s, s.c);
+}
+__device__ __forceinline__ uint32_t q8_pair_f32(const __bf16*, float u0, float u1, Q8ScaleF32 s) {
+    return Op<__bf16>::cvt2(__builtin_fmaf(u0, s.s, s.c), __builtin_fmaf(u1, s.s, s.c));  // one v_cvt_pk_bf16_f32
+}
+
+template <typename T>
+__device__ __forceinline__ typename Q8Mfma<T>::V8 q8_dequant8_f32(uint32_t w0, uint32_t w1, Q8ScaleF32 s) {
+    const T* tag = nullptr;
+    uint32_t o[4];
+#pragma unroll
+    for (int d = 0; d < 2; d++) {
+        const uint32_t x = d ? w1 : w0;
+        o[2 * d] = q8_pair_f32(tag, (float)(x & 0xffu), (float)((x >> 8) & 0xffu), s);
+        o[2 * d + 1] = q8_pair_f32(tag, (float)((x >> 16) & 0xffu), (float)(x >> 24), s);
+    }
+    return __builtin_bit_cast(typename Q8Mfma<T>::V8, u32x4{o[0], o[1], o[2], o[3]});
+}
+
+// f32 scales, either operand type
+template <typename T>
+struct Q8Op<T, true> : Q8Mfma<T> {
+    typedef Q8ScaleF32 Scale;
+    static __device__ __forceinline__ Scale scale(uint32_t word) {
+        const float s = __builtin_bit_cast(float, word);
+        return Scale{s, -128.0f * s};
+    }
+    static __device__ __forceinline__ typename Q8Mfma<T>::V8 deq8(uint32_t w0, uint32_t w1, Scale s) {
+        return q8_dequant8_f32<T>(w0, w1, s);
+    }
 };
 
 template <>
-struct Q8Op<__bf16> {
+struct Q8Op<_Float16, false> : Q8Mfma<_Float16> {
+    typedef f16x2 Scale;  // the f16 scale in both halves
+    static __device__ __forceinline__ Scale scale(uint32_t pair) { return __builtin_bit_cast(f16x2, pair); }
+    static __device__ __forceinline__ V8 deq8(uint32_t w0, uint32_t w1, Scale s) { return q8_dequant8(w0, w1, s); }
+};
+
+// bf16 operands, f16 scales: the f32 path with the scale widened exactly
+template <>
+struct Q8Op<__bf16, false> : Q8Mfma<__bf16> {
     typedef Q8ScaleF32 Scale;
-    typedef bf16x8 V8;
     static __device__ __forceinline__ Scale scale(uint32_t pair) {
         const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)(pair & 0xffffu));
         return Scale{s, -128.0f * s};
     }
     static __device__ __forceinline__ V8 deq8(uint32_t w0, uint32_t w1, Scale s) {
-        uint32_t o[4];
-#pragma unroll
-        for (int d = 0; d < 2; d++) {
-            const uint32_t x = d ? w1 : w0;
-            const float f0 = __builtin_fmaf((float)(x & 0xffu), s.s, s.c);
-            const float f1 = __builtin_fmaf((float)((x >> 8) & 0xffu), s.s, s.c);
-            const float f2 = __builtin_fmaf((float)((x >> 16) & 0xffu), s.s, s.c);
-            const float f3 = __builtin_fmaf((float)(x >> 24), s.s, s.c);
-            o[2 * d] = Op<__bf16>::cvt2(f0, f1);
-            o[2 * d + 1] = Op<__bf16>::cvt2(f2, f3);
-        }
-        return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
-    }
-    static __device__ __forceinline__ f32x16 mfma(u32x4 a, V8 b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
+        return q8_dequant8_f32<__bf16>(w0, w1, s);
     }
 };
 
 // Raw buffer descriptor word 3 for gfx9-family parts (untyped dword access).
 #define Q8_RSRC_W3 0x00020000
 
-template <typename T, int EPI, bool PP>
+template <typename T, bool SF32, int EPI, bool PP>
 struct Q8Gemm {
-    typedef Q8Op<T> QO;
+    typedef Q8Op<T, SF32> QO;
     static constexpr int NI = 4, NJ = 2;
     const LtxGemmArgs& a;
     f32x16 acc[NI][NJ];
@@ -333,12 +371,12 @@ struct Q8Gemm {
     }
 };
 
-#define Q8_GEMM_KERNEL(NAME, T_, EPI_)                                                       \
+#define Q8_GEMM_KERNEL(NAME, T_, SF32_, EPI_)                                                \
     extern "C" __global__ void __launch_bounds__(512, 1) NAME(const LtxGemmArgs a) {         \
-        Q8Gemm<T_, EPI_, false> k(a);                                                        \
+        Q8Gemm<T_, SF32_, EPI_, false> k(a);                                                 \
         k.run();                                                                             \
     }                                                                                        \
     extern "C" __global__ void __launch_bounds__(512, 1) NAME##_pp(const LtxGemmArgs a) {    \
-        Q8Gemm<T_, EPI_, true> k(a);                                                         \
+        Q8Gemm<T_, SF32_, EPI_, true> k(a);                                                  \
         k.run();                                                                             \
     }

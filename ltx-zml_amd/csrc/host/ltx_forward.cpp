@@ -141,12 +141,13 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
     // LDS-DMA int8 kernel: f16 or bf16 operands, f16 scales, K a multiple of
     // 128, and byte offsets of A and W within 31 bits (32-bit buffer offsets)
     auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
-    if ((mode == LTX_MODE_F16 || mode == LTX_MODE_BF16) && p.q8 && p.qflip && p.scale_f16 && p.s2.p &&
+    if ((mode == LTX_MODE_F16 || mode == LTX_MODE_BF16) && p.q8 && p.qflip && p.s2.p &&
         c->gemm_q8 != 0 && p.K % 128 == 0 && (uint64_t)M * lda * 2 < (1ull << 31) && (uint64_t)p.N * p.K < (1ull << 31) && g.ldo % 8 == 0 &&
         al16(g.out) && al16(g.out2) && al16(g.resid) && al16(g.bias) && al16(g.ada.tstab) && al16(g.ada.sst)) {
         // (its epilogue moves 16-byte vectors: outputs, residual and bias 16-byte aligned)
         g.scales = p.s2.p;
-        std::snprintf(name, sizeof(name), "ltx_gemm_q8_%s%s%s", mode == LTX_MODE_BF16 ? "bf16_" : "",
+        std::snprintf(name, sizeof(name), "ltx_gemm_q8_%s%s%s%s", mode == LTX_MODE_BF16 ? "bf16_" : "",
+                      p.scale_f16 ? "" : "s32_",
                       epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv",
                       c->gemm_q8 == 2 ? "_pp" : "");
         const int ntiles = g.tiles_m * g.tiles_n;
@@ -432,11 +433,11 @@ int ltx_op_linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* sca
                 ltx::gemm32(c, p, 0, N, (const float*)a, M, (float*)y, LTX_EPI_STORE, nullptr, ada, 0, gelu,
                             (hipStream_t)stream);
             } else {
-                if (scale_f16 && c->gemm_q8 != 0 && N % 256 == 0) {
-                    // the LDS-DMA kernel reads scale pairs [K/128][N]
+                if (c->gemm_q8 != 0 && N % 256 == 0) {
+                    // the LDS-DMA kernel reads scale words [K/128][N]
                     const size_t n2 = (size_t)N * (K / LTX_GROUP);
                     if (c->op_pairs.bytes < n2 * 4) c->op_pairs.alloc(n2 * 4);
-                    LtxPairArgs pa{(const uint16_t*)scales, (uint32_t*)c->op_pairs.p, N, K / LTX_GROUP};
+                    LtxPairArgs pa{scales, (uint32_t*)c->op_pairs.p, N, K / LTX_GROUP, scale_f16 ? 0 : 1};
                     c->launch("ltx_scale_pairs", (unsigned)((n2 + 255) / 256), 1, 1, 256, &pa, (hipStream_t)stream);
                     p.s2.p = c->op_pairs.p;
                     // and its weights as the bytes q + 128

@@ -50,7 +50,7 @@ struct LtxProj {
     int scale_f16 = 0;
     ltx::DevBuf q;            // int8 [N][K]
     ltx::DevBuf s;            // [N][K/128] f32 or f16
-    ltx::DevBuf s2;           // f16 scales only: u32 [K/128][N], each the scale in both halves
+    ltx::DevBuf s2;           // scale words u32 [K/128][N]: an f16 scale in both halves, or f32 bits
     ltx::DevBuf w_bf16;       // bf16 [N][K] (base tensor)
     ltx::DevBuf w_f16;        // f16 copy of the base tensor (F16 mode, non-q8)
     ltx::DevBuf bias;         // f32 [N] (may be empty)

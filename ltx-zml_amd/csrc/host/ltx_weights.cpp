@@ -102,11 +102,20 @@ static void build_proj(LtxProj& p, const void* const* base, const int8_t* const*
         h2d(p.q, q.data(), q.size() * 8);
         p.qflip = true;
         h2d(p.s, s.data(), s.size());
-        if (sf16) {  // f16 scales also as pairs (s | s << 16), u32 [G][N], for the LDS-DMA kernels
-            const uint16_t* s16 = (const uint16_t*)s.data();
+        {  // the scales also as words u32 [G][N] for the LDS-DMA kernels: f16 pairs (s | s << 16) or f32 bits
             std::vector<uint32_t> s2((size_t)G * p.N);
             for (size_t n = 0; n < (size_t)p.N; n++)
-                for (size_t g = 0; g < G; g++) s2[g * p.N + n] = (uint32_t)s16[n * G + g] * 0x10001u;
+                for (size_t g = 0; g < G; g++) {
+                    uint32_t w = 0;
+                    if (sf16) {
+                        uint16_t h;
+                        std::memcpy(&h, s.data() + 2 * (n * G + g), 2);
+                        w = (uint32_t)h * 0x10001u;
+                    } else {
+                        std::memcpy(&w, s.data() + 4 * (n * G + g), 4);
+                    }
+                    s2[g * p.N + n] = w;
+                }
             h2d(p.s2, s2.data(), s2.size() * 4);
         }
     } else {
@@ -363,11 +372,9 @@ struct DevCarve {
                 r += Ns[j];
             }
             p.qflip = true;
-            if (L.sf16) {
-                ensure(p.s2, G * p.N * 4);
-                LtxPairArgs pa{(const uint16_t*)p.s.p, (uint32_t*)p.s2.p, p.N, (int)G};
-                c->launch("ltx_scale_pairs", (unsigned)((G * p.N + 255) / 256), 1, 1, 256, &pa, st);
-            }
+            ensure(p.s2, G * p.N * 4);
+            LtxPairArgs pa{p.s.p, (uint32_t*)p.s2.p, p.N, (int)G, L.sf16 ? 0 : 1};
+            c->launch("ltx_scale_pairs", (unsigned)((G * p.N + 255) / 256), 1, 1, 256, &pa, st);
         } else {
             ensure(p.w_bf16, (size_t)p.N * K * 2);
             size_t r = 0;

@@ -175,15 +175,21 @@ GEMM_KERNEL(ltx_gemm_bf16_i8f16_qkv, __bf16, LTX_B_I8_F16S, LTX_EPI_QKV)
 GEMM_KERNEL(ltx_gemm_bf16_w16_store, __bf16, LTX_B_W16, LTX_EPI_STORE)
 GEMM_KERNEL(ltx_gemm_bf16_w16_resid, __bf16, LTX_B_W16, LTX_EPI_RESID_GATE)
 
-// LDS-DMA W8A16 kernels (f16 scales): ltx_gemm_q8_{store,resid,qkv} for f16
-// operands, ltx_gemm_q8_bf16_{store,resid,qkv} for bf16 operands, and the
-// ping-pong variants with suffix _pp.
-Q8_GEMM_KERNEL(ltx_gemm_q8_store, _Float16, LTX_EPI_STORE)
-Q8_GEMM_KERNEL(ltx_gemm_q8_resid, _Float16, LTX_EPI_RESID_GATE)
-Q8_GEMM_KERNEL(ltx_gemm_q8_qkv, _Float16, LTX_EPI_QKV)
-Q8_GEMM_KERNEL(ltx_gemm_q8_bf16_store, __bf16, LTX_EPI_STORE)
-Q8_GEMM_KERNEL(ltx_gemm_q8_bf16_resid, __bf16, LTX_EPI_RESID_GATE)
-Q8_GEMM_KERNEL(ltx_gemm_q8_bf16_qkv, __bf16, LTX_EPI_QKV)
+// LDS-DMA W8A16 kernels: ltx_gemm_q8_[bf16_][s32_]{store,resid,qkv}[_pp] for
+// f16 (bf16_: bf16) operands with f16 (s32_: f32) scales; _pp is the
+// ping-pong schedule.
+Q8_GEMM_KERNEL(ltx_gemm_q8_store, _Float16, false, LTX_EPI_STORE)
+Q8_GEMM_KERNEL(ltx_gemm_q8_resid, _Float16, false, LTX_EPI_RESID_GATE)
+Q8_GEMM_KERNEL(ltx_gemm_q8_qkv, _Float16, false, LTX_EPI_QKV)
+Q8_GEMM_KERNEL(ltx_gemm_q8_bf16_store, __bf16, false, LTX_EPI_STORE)
+Q8_GEMM_KERNEL(ltx_gemm_q8_bf16_resid, __bf16, false, LTX_EPI_RESID_GATE)
+Q8_GEMM_KERNEL(ltx_gemm_q8_bf16_qkv, __bf16, false, LTX_EPI_QKV)
+Q8_GEMM_KERNEL(ltx_gemm_q8_s32_store, _Float16, true, LTX_EPI_STORE)
+Q8_GEMM_KERNEL(ltx_gemm_q8_s32_resid, _Float16, true, LTX_EPI_RESID_GATE)
+Q8_GEMM_KERNEL(ltx_gemm_q8_s32_qkv, _Float16, true, LTX_EPI_QKV)
+Q8_GEMM_KERNEL(ltx_gemm_q8_bf16_s32_store, __bf16, true, LTX_EPI_STORE)
+Q8_GEMM_KERNEL(ltx_gemm_q8_bf16_s32_resid, __bf16, true, LTX_EPI_RESID_GATE)
+Q8_GEMM_KERNEL(ltx_gemm_q8_bf16_s32_qkv, __bf16, true, LTX_EPI_QKV)
 
 // Gate logits (ltx/block.zig:238, 526, 564): glog[t][h] = a[t] . gw[h] + gb[h].
 // One wave per 32 token rows: 256 MFMAs over K = 4096, operands straight

@@ -332,5 +332,6 @@ extern "C" __global__ void __launch_bounds__(256) ltx_scale_pairs(const LtxPairA
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= a.N * a.G) return;
     const int g = i / a.N, n = i - g * a.N;
-    a.out[i] = (uint32_t)a.s[(size_t)n * a.G + g] * 0x10001u;
+    const size_t j = (size_t)n * a.G + g;
+    a.out[i] = a.f32 ? ((const uint32_t*)a.s)[j] : (uint32_t)((const uint16_t*)a.s)[j] * 0x10001u;
 }

@@ -155,12 +155,13 @@ typedef struct {
     size_t n;
 } LtxFlipArgs;
 
-// f16 scales [N][G] -> scale pairs u32 [G][N] (s | s << 16) for the LDS-DMA
-// int8 GEMM.
+// Scales [N][G] -> scale words u32 [G][N] for the LDS-DMA int8 GEMM: f16
+// scales as pairs (s | s << 16), f32 scales (f32 != 0) as their bits.
 typedef struct {
-    const uint16_t* s;
+    const void* s;
     uint32_t* out;
     int N, G;
+    int f32;
 } LtxPairArgs;
 
 // f32 reference-precision kernels (mode LTX_MODE_F32).

@@ -107,13 +107,15 @@ def test_linear_q8(ctx, mode, M, N, K, gelu, out_f32, scale_f16):
     assert oracle.rel_rms(got, exact_w) <= (1e-3 if mode == "f16" else 6e-3)
 
 
-def _onehot_case(ctx, M, N, K, seed, mode="f16"):
+def _onehot_case(ctx, M, N, K, seed, mode="f16", sf32=False):
     """y = E . W^T with E[m][k] = (k == m mod K): every output is one weight
-    operand times 1, so y must equal the 16-bit operand RNE16(q * s) bit for
-    bit (one nonzero product, f32 accumulation)."""
+    operand times 1, so y must equal the 16-bit operand bit for bit (one
+    nonzero product, f32 accumulation): f16 one rounding of the exact q * s,
+    bf16 RNE of the f32 value f32(q) * s (as the dequant probe); with f16
+    scales q * s is exact in f32 and the two definitions agree."""
     rng = np.random.default_rng(seed)
     q = rng.integers(-128, 128, size=(N, K), dtype=np.int16).astype(np.int8)
-    s = (10.0 ** rng.uniform(-4, -1, size=(N, K // 128))).astype(np.float16)
+    s = (10.0 ** rng.uniform(-4, -1, size=(N, K // 128))).astype(np.float32 if sf32 else np.float16)
     e = np.zeros((M, K), np.float32)
     e[np.arange(M), np.arange(M) % K] = 1.0
     dq, ds = torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda()
@@ -121,7 +123,7 @@ def _onehot_case(ctx, M, N, K, seed, mode="f16"):
     m, dt = MODES[mode]
     ctx.linear_q8(to16(e, dt).cuda(), dq, ds, None, y, mode=m)
     torch.cuda.synchronize()
-    exact = q.astype(np.float64) * np.repeat(s.astype(np.float64), 128, axis=1)  # exact in f32 too
+    exact = q.astype(np.float64) * np.repeat(s.astype(np.float64), 128, axis=1)  # exact: 8 x 24 bits
     if mode == "f16":
         op = exact.astype(np.float16).astype(np.float32)
     else:
@@ -130,11 +132,12 @@ def _onehot_case(ctx, M, N, K, seed, mode="f16"):
     return y.cpu().numpy(), want
 
 
+@pytest.mark.parametrize("sf32", [False, True])
 @pytest.mark.parametrize("mode", ["f16", "bf16"])
 @pytest.mark.parametrize("M,N,K", [(1024, 512, 1024), (300, 256, 256)])
-def test_linear_q8_onehot_exact(ctx, M, N, K, mode):
-    say(f"linear_q8 one-hot {mode} M={M} N={N} K={K}")
-    got, want = _onehot_case(ctx, M, N, K, seed=M + K, mode=mode)
+def test_linear_q8_onehot_exact(ctx, M, N, K, mode, sf32):
+    say(f"linear_q8 one-hot {mode} M={M} N={N} K={K} f32 scales={sf32}")
+    got, want = _onehot_case(ctx, M, N, K, seed=M + K, mode=mode, sf32=sf32)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
@@ -147,8 +150,9 @@ def test_linear_q8_variants(monkeypatch, variant):
     c = rt.Context(0)
     try:
         for mode in ("f16", "bf16"):
-            got, want = _onehot_case(c, 1024, 512, 1024, seed=9, mode=mode)
-            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), mode
+            for sf32 in (False, True):
+                got, want = _onehot_case(c, 1024, 512, 1024, seed=9, mode=mode, sf32=sf32)
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (mode, sf32)
         a, q, s, b = _gemm_case(300, 768, 4096, seed=11, scale_f16=True)
         y = torch.empty((300, 768), dtype=torch.float32, device="cuda")
         c.linear_q8(to16(a, torch.float16).cuda(), torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(),
