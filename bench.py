@@ -251,6 +251,9 @@ def main() -> int:
     ap.add_argument("--denoise", type=int, default=0, metavar="BLOCKS",
                     help="instead of the block line: time the stage-1 denoising loop (8 Euler steps) over this "
                          "many resident blocks (48 for the whole transformer) and print its own JSON line")
+    ap.add_argument("--scales", default="f16", choices=["f16", "f32"],
+                    help="scale type of the int8 weights: fp16 (the benchmark configuration) or f32 (the "
+                         "reference packer's version-1 format)")
     ap.add_argument("--sweep", action="store_true",
                     help="instead of the block line: time the isolated GEMM and attention kernels at the "
                          "microbenchmark shapes (f16 and bf16 operands) and print their own JSON line")
@@ -275,7 +278,7 @@ def main() -> int:
     if args.sweep:
         return sweep_bench(args)
     t0 = time.time()
-    bt = synth.make_block(0, seed=1, dist="t3", classes=("qkv", "ff", "out"), scale_dtype="F16")
+    bt = synth.make_block(0, seed=1, dist="t3", classes=("qkv", "ff", "out"), scale_dtype=args.scales.upper())
     inp = synth.make_inputs(T, S, sigma=0.7)
     cos, sin = rt.rope_tables(inp["grid"])
     log(f"bench: inputs ready in {time.time() - t0:.1f}s (T={T}, S={S})")
@@ -333,7 +336,7 @@ def main() -> int:
         "ms_per_step": round(ms, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16" if args.mode == "f16" else "bf16",
-        "weights": "int8 grouped-128, fp16 scales",
+        "weights": "int8 grouped-128, " + ("fp16" if args.scales == "f16" else "f32") + " scales",
         "data": "synthetic",
         "config": {"workload": "LTX-2.5 DiT block forward, int8 weights", "tokens": T, "latent_grid": [14, 32, 64],
                    "text_tokens": S, "d_model": D, "heads": H, "head_dim": HD, "ffn": FF, "sigma": 0.7,

@@ -136,7 +136,7 @@ __device__ __forceinline__ typename Q8Mfma<T>::V8 q8_dequant8_f32(uint32_t w0, u
     return __builtin_bit_cast(typename Q8Mfma<T>::V8, u32x4{o[0], o[1], o[2], o[3]});
 }
 
-// f32 scales, either operand type
+// f32 scales through f32 (bf16 operands; f16 operands have their own form below)
 template <typename T>
 struct Q8Op<T, true> : Q8Mfma<T> {
     typedef Q8ScaleF32 Scale;
@@ -146,6 +146,37 @@ struct Q8Op<T, true> : Q8Mfma<T> {
     }
     static __device__ __forceinline__ typename Q8Mfma<T>::V8 deq8(uint32_t w0, uint32_t w1, Scale s) {
         return q8_dequant8_f32<T>(w0, w1, s);
+    }
+};
+
+// f16 operands, f32 scales: each byte u enters as the f16 subnormal u 2^-24
+// (one v_perm per pair, exact), and fma(u 2^-24, s 2^24, -128 s) = q s is
+// rounded once to f16 by v_fma_mix reading that f16 directly: the rounding
+// of the exact q * s that the register-staged kernels make, in 3 VALU
+// instructions per MFMA. s 2^24 is finite for |s| < 2^104; above
+// 65504 / 128 every nonzero q * s is beyond the f16 range anyway.
+template <>
+struct Q8Op<_Float16, true> : Q8Mfma<_Float16> {
+    typedef Q8ScaleF32 Scale;  // s 2^24 and -128 s
+    static __device__ __forceinline__ Scale scale(uint32_t word) {
+        const float s = __builtin_bit_cast(float, word);
+        return Scale{s * 16777216.0f, -128.0f * s};
+    }
+    static __device__ __forceinline__ V8 deq8(uint32_t w0, uint32_t w1, Scale s) {
+        uint32_t o[4];
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+            const uint32_t x = d ? w1 : w0;
+            const f16x2 p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0u, x, 0x04010400u));
+            const f16x2 p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0u, x, 0x04030402u));
+            const f16x2 r0 = {(_Float16)__builtin_fmaf((float)p0[0], s.s, s.c),
+                              (_Float16)__builtin_fmaf((float)p0[1], s.s, s.c)};
+            const f16x2 r1 = {(_Float16)__builtin_fmaf((float)p1[0], s.s, s.c),
+                              (_Float16)__builtin_fmaf((float)p1[1], s.s, s.c)};
+            o[2 * d] = __builtin_bit_cast(uint32_t, r0);
+            o[2 * d + 1] = __builtin_bit_cast(uint32_t, r1);
+        }
+        return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
     }
 };
 
