@@ -136,7 +136,8 @@ __device__ __forceinline__ typename Q8Mfma<T>::V8 q8_dequant8_f32(uint32_t w0, u
     return __builtin_bit_cast(typename Q8Mfma<T>::V8, u32x4{o[0], o[1], o[2], o[3]});
 }
 
-// f32 scales through f32 (bf16 operands; f16 operands have their own form below)
+// f32 scales through f32 (bf16 operands, where q * s may be as large as the
+// f32 range: no prescaled form; f16 operands have their own form below)
 template <typename T>
 struct Q8Op<T, true> : Q8Mfma<T> {
     typedef Q8ScaleF32 Scale;
@@ -187,16 +188,30 @@ struct Q8Op<_Float16, false> : Q8Mfma<_Float16> {
     static __device__ __forceinline__ V8 deq8(uint32_t w0, uint32_t w1, Scale s) { return q8_dequant8(w0, w1, s); }
 };
 
-// bf16 operands, f16 scales: the f32 path with the scale widened exactly
+// bf16 operands, f16 scales: each byte u as the f16 subnormal u 2^-24 (one
+// v_perm per pair), v_fma_mix_f32 reads it directly and forms
+// fma(u 2^-24, s 2^24, -128 s) = q s (exact in f32: at most 19 significant
+// bits), one v_cvt_pk_bf16_f32 rounds the pair; 4 VALU instructions per
+// MFMA. s 2^24 of an f16 scale is at most 1.1e12.
 template <>
 struct Q8Op<__bf16, false> : Q8Mfma<__bf16> {
-    typedef Q8ScaleF32 Scale;
+    typedef Q8ScaleF32 Scale;  // s 2^24 and -128 s
     static __device__ __forceinline__ Scale scale(uint32_t pair) {
         const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)(pair & 0xffffu));
-        return Scale{s, -128.0f * s};
+        return Scale{s * 16777216.0f, -128.0f * s};
     }
     static __device__ __forceinline__ V8 deq8(uint32_t w0, uint32_t w1, Scale s) {
-        return q8_dequant8_f32<__bf16>(w0, w1, s);
+        uint32_t o[4];
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+            const uint32_t x = d ? w1 : w0;
+            const f16x2 p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0u, x, 0x04010400u));
+            const f16x2 p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0u, x, 0x04030402u));
+            o[2 * d] = Op<__bf16>::cvt2(__builtin_fmaf((float)p0[0], s.s, s.c), __builtin_fmaf((float)p0[1], s.s, s.c));
+            o[2 * d + 1] =
+                Op<__bf16>::cvt2(__builtin_fmaf((float)p1[0], s.s, s.c), __builtin_fmaf((float)p1[1], s.s, s.c));
+        }
+        return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
     }
 };
 
