@@ -15,17 +15,24 @@
 // every wave dequantises the fragments it reads (half the LDS bytes of an f16
 // tile, no second LDS pass).
 //
-// Dequantisation is exact: the weight bytes are stored as u = q + 128 (q XOR
-// 0x80, done once at upload), the f16 with bits 0x6400 | u is 1024 + u;
-// subtracting 1152 gives q exactly and one f16 multiply by the f16 scale
-// rounds q * s once to nearest even — the operand RNE16(q * s) that the
-// register-staged kernels also feed the MFMA. For bf16 operands (no packed
-// bf16 multiply on gfx950) and for f32 scales, each byte u goes to f32
-// exactly (v_cvt_f32_ubyteN) and the staging arithmetic of the
-// register-staged kernels follows: f16 operands take one rounding of the
-// exact fma(u, s, -128 s) = q * s (v_fma_mix), bf16 operands the RNE of its
-// f32 value f32(q) * s, the reference's dequantised weight. With f16 scales
-// q * s is exact in f32 (at most 19 significant bits) and the two agree.
+// Dequantisation is exact. The weight bytes are stored as u = q + 128 (q XOR
+// 0x80, done once at upload); the operand is the one the register-staged
+// kernels and the dequant probe produce: for f16, q * s rounded once to
+// nearest even; for bf16, the f32 value f32(q) * s (the reference's
+// dequantised weight) rounded to nearest even. Per operand and scale type:
+// - f16, f16 scales: the f16 with bits 0x6400 | u is 1024 + u; subtracting
+//   1152 gives q exactly, one v_pk_mul_f16 by the scale rounds q * s once
+//   (v_perm, v_pk_add_f16, v_pk_mul_f16: 3 VALU instructions per MFMA).
+// - f16, f32 scales: the f16 with bits u is the subnormal u 2^-24;
+//   v_fma_mixlo/hi_f16 reads it and rounds fma(u 2^-24, s 2^24, -128 s) =
+//   q * s once (3 per MFMA; s 2^24 is finite for |s| < 2^104, and above
+//   65504 / 128 every nonzero q * s is beyond the f16 range anyway).
+// - bf16, f16 scales: the same subnormal read by v_fma_mix_f32 gives q * s
+//   in f32 (exact: at most 19 significant bits), one v_cvt_pk_bf16_f32
+//   rounds a pair (4 per MFMA).
+// - bf16, f32 scales: v_cvt_f32_ubyteN and v_fma_f32 (u, s, -128 s) give
+//   f32(q) * s for scales spanning the whole f32 range, then
+//   v_cvt_pk_bf16_f32 (5 per MFMA).
 //
 // LDS layout: A rows of 128 B (8 chunks of 8 k), chunk c of row r stored in
 // slot c ^ ((r >> 1) & 7) (16 consecutive rows, one ds_read_b128 lane group,
