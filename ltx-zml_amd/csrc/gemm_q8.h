@@ -120,40 +120,32 @@ struct Q8ScaleF32 {
     float s, c;  // the scale and -128 times it (exact: a power of two)
 };
 
-// 8 weights through fma(u, s, -128 s), the staging arithmetic of the
-// register-staged kernels and the dequant probe (deq_pack2): for f16 one
-// rounding of the exact q * s (v_fma_mix), for bf16 RNE of the f32 value.
-__device__ __forceinline__ uint32_t q8_pair_f32(const _Float16*, float u0, float u1, Q8ScaleF32 s) {
-    return deq_pack2<_Float16>(u0, u1, s.s, s.c);
-}
-__device__ __forceinline__ uint32_t q8_pair_f32(const __bf16*, float u0, float u1, Q8ScaleF32 s) {
-    return Op<__bf16>::cvt2(__builtin_fmaf(u0, s.s, s.c), __builtin_fmaf(u1, s.s, s.c));  // one v_cvt_pk_bf16_f32
-}
-
-template <typename T>
-__device__ __forceinline__ typename Q8Mfma<T>::V8 q8_dequant8_f32(uint32_t w0, uint32_t w1, Q8ScaleF32 s) {
-    const T* tag = nullptr;
+// 8 weights to bf16 through f32: fma(u, s, -128 s) = f32(q * s), then one
+// v_cvt_pk_bf16_f32 per pair.
+__device__ __forceinline__ bf16x8 q8_dequant8_bf16_f32(uint32_t w0, uint32_t w1, Q8ScaleF32 s) {
     uint32_t o[4];
 #pragma unroll
     for (int d = 0; d < 2; d++) {
         const uint32_t x = d ? w1 : w0;
-        o[2 * d] = q8_pair_f32(tag, (float)(x & 0xffu), (float)((x >> 8) & 0xffu), s);
-        o[2 * d + 1] = q8_pair_f32(tag, (float)((x >> 16) & 0xffu), (float)(x >> 24), s);
+        o[2 * d] = Op<__bf16>::cvt2(__builtin_fmaf((float)(x & 0xffu), s.s, s.c),
+                                    __builtin_fmaf((float)((x >> 8) & 0xffu), s.s, s.c));
+        o[2 * d + 1] = Op<__bf16>::cvt2(__builtin_fmaf((float)((x >> 16) & 0xffu), s.s, s.c),
+                                        __builtin_fmaf((float)(x >> 24), s.s, s.c));
     }
-    return __builtin_bit_cast(typename Q8Mfma<T>::V8, u32x4{o[0], o[1], o[2], o[3]});
+    return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
 }
 
-// f32 scales through f32 (bf16 operands, where q * s may be as large as the
-// f32 range: no prescaled form; f16 operands have their own form below)
-template <typename T>
-struct Q8Op<T, true> : Q8Mfma<T> {
+// bf16 operands, f32 scales: through f32 without a prescaled form, since
+// q * s may span the whole f32 range
+template <>
+struct Q8Op<__bf16, true> : Q8Mfma<__bf16> {
     typedef Q8ScaleF32 Scale;
     static __device__ __forceinline__ Scale scale(uint32_t word) {
         const float s = __builtin_bit_cast(float, word);
         return Scale{s, -128.0f * s};
     }
-    static __device__ __forceinline__ typename Q8Mfma<T>::V8 deq8(uint32_t w0, uint32_t w1, Scale s) {
-        return q8_dequant8_f32<T>(w0, w1, s);
+    static __device__ __forceinline__ V8 deq8(uint32_t w0, uint32_t w1, Scale s) {
+        return q8_dequant8_bf16_f32(w0, w1, s);
     }
 };
 
