@@ -107,7 +107,7 @@ def test_linear_q8(ctx, mode, M, N, K, gelu, out_f32, scale_f16):
     assert oracle.rel_rms(got, exact_w) <= (1e-3 if mode == "f16" else 6e-3)
 
 
-def _onehot_case(ctx, M, N, K, seed, mode="f16", sf32=False):
+def _onehot_case(ctx, M, N, K, seed, mode="f16", sf32=False, exp_range=(-4, -1)):
     """y = E . W^T with E[m][k] = (k == m mod K): every output is one weight
     operand times 1, so y must equal the 16-bit operand bit for bit (one
     nonzero product, f32 accumulation): f16 one rounding of the exact q * s,
@@ -115,7 +115,7 @@ def _onehot_case(ctx, M, N, K, seed, mode="f16", sf32=False):
     scales q * s is exact in f32 and the two definitions agree."""
     rng = np.random.default_rng(seed)
     q = rng.integers(-128, 128, size=(N, K), dtype=np.int16).astype(np.int8)
-    s = (10.0 ** rng.uniform(-4, -1, size=(N, K // 128))).astype(np.float32 if sf32 else np.float16)
+    s = (10.0 ** rng.uniform(*exp_range, size=(N, K // 128))).astype(np.float32 if sf32 else np.float16)
     e = np.zeros((M, K), np.float32)
     e[np.arange(M), np.arange(M) % K] = 1.0
     dq, ds = torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda()
@@ -139,6 +139,21 @@ def test_linear_q8_onehot_exact(ctx, M, N, K, mode, sf32):
     say(f"linear_q8 one-hot {mode} M={M} N={N} K={K} f32 scales={sf32}")
     got, want = _onehot_case(ctx, M, N, K, seed=M + K, mode=mode, sf32=sf32)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("mode,exp_range", [
+    ("f16", (-9, -5)),   # q * s among the f16 subnormals: one rounding into them
+    ("bf16", (20, 36)),  # q * s up to 1.3e38: the bf16 path keeps the whole f32 range
+])
+def test_linear_q8_onehot_extreme_f32_scales(ctx, mode, exp_range):
+    """Values, not bits: an operand that underflows to -0 leaves the f32
+    accumulation (+0 + 1 * -0) as +0."""
+    say(f"linear_q8 one-hot {mode} f32 scales 1e{exp_range[0]}..1e{exp_range[1]}")
+    got, want = _onehot_case(ctx, 1024, 512, 1024, seed=21, mode=mode, sf32=True, exp_range=exp_range)
+    assert np.isfinite(want).all()
+    assert np.array_equal(got, want)
+    if mode == "f16":
+        assert ((want != 0) & (np.abs(want) < 6.1e-5)).sum() > 1000  # subnormal operands were exercised
 
 
 @pytest.mark.parametrize("variant", ["reg", "dma"])
