@@ -1,5 +1,6 @@
 """The block at its full size (T = 28,672 tokens on the (14, 32, 64) grid,
-S = 256, every projection int8 with f16 scales, fp16 and bf16 MFMA modes),
+S = 256, every projection int8 with f16 scales, fp16 and bf16 MFMA modes,
+and with the f32 scales of the reference's own format in fp16 mode),
 checked where an f64 reference is affordable:
 
 - self-attention: 64 query rows (spread over the sequence) of the gated,
@@ -44,6 +45,14 @@ def full():
     return bt, inp, cos, sin
 
 
+@pytest.fixture(scope="module")
+def full_s32(full):
+    """The same block with the f32 scales of the reference's own format."""
+    _, inp, cos, sin = full
+    bt = synth.make_block(0, seed=1, dist="t3", classes=("qkv", "ff", "out"), scale_dtype="F32")
+    return bt, inp, cos, sin
+
+
 def _run(ctx, w, inp, cos, sin, mode=rt.MODE_F16):
     y = torch.empty((T, 4096), dtype=torch.float32, device="cuda")
     ctx.forward(w, dev(inp["x"]), dev(inp["tstab"]), dev(inp["tidx"]), dev(inp["ctx"]), dev(inp["pts2"]), dev(cos),
@@ -62,10 +71,10 @@ def _stage(ctx, name, dtype, shape, rows=None):
 GATES = {"f16": (2e-3, 2e-3), "bf16": (1e-2, 6e-3)}  # attention rows, ff1 rows
 
 
-@pytest.mark.parametrize("mode", ["f16", "bf16"])
-def test_full_size_block(ctx, full, mode):
-    bt, inp, cos, sin = full
-    say(f"full-size block T={T} S={S} {mode}: forward, determinism, attention and FFN rows")
+@pytest.mark.parametrize("mode,scales", [("f16", "f16"), ("bf16", "f16"), ("f16", "f32")])
+def test_full_size_block(ctx, request, mode, scales):
+    bt, inp, cos, sin = request.getfixturevalue("full" if scales == "f16" else "full_s32")
+    say(f"full-size block T={T} S={S} {mode} operands, {scales} scales: forward, determinism, attention and FFN rows")
     m = rt.MODES[mode]
     dt = torch.float16 if mode == "f16" else torch.bfloat16
     w = ctx.upload(bt)
@@ -98,7 +107,8 @@ def test_full_size_block(ctx, full, mode):
     hpre = ff_in @ wf.T
     hw = 0.5 * hpre * (1 + np.tanh(np.sqrt(2 / np.pi) * (hpre + 0.044715 * hpre ** 3)))
     r_ff = oracle.rel_rms(ff_h, hw)
-    print(f"full size {mode}: attention rows rel-RMS {r_att:.3e}, ff1+gelu rows rel-RMS {r_ff:.3e}", flush=True)
+    print(f"full size {mode}/{scales}: attention rows rel-RMS {r_att:.3e}, ff1+gelu rows rel-RMS {r_ff:.3e}",
+          flush=True)
     g_att, g_ff = GATES[mode]
     assert r_att <= g_att and r_ff <= g_ff
 
