@@ -78,7 +78,10 @@ const char* ltx_version(void);
  * (ltx/loader.zig:100-129). `mem` is the blob bytes (an mmap or a ring slot),
  * `manifest_json` the text of blob_manifest.json. q8scale entries may be F32
  * (the reference format) or F16. Missing q8 entries fall back to the bf16
- * base weight for that projection. */
+ * base weight for that projection. Entries must lie inside `mem` at offsets
+ * that are multiples of the manifest's alignment, and F32 scales must be
+ * finite with magnitude below 2^100 (error "ScaleRange"; absmax / 127 of any
+ * bf16 weight below 1e32 is). */
 int ltx_block_weights_from_blob(ltx_ctx* ctx, const void* mem, uint64_t mem_bytes, const char* manifest_json,
                                 int64_t block_idx, ltx_block_weights** out);
 
@@ -123,8 +126,10 @@ int ltx_block_forward(ltx_ctx* ctx, const ltx_block_weights* w, const float* x, 
                       const float* sin, int T, float* y, int mode, void* stream);
 
 /* Intermediate tensors of the last forward, for staged parity checks
- * (the staged methods of ltx/block.zig:248-338). Device pointer + bytes,
- * valid until the next forward on this context. */
+ * (the staged methods of ltx/block.zig:248-338), and the velocity of the last
+ * ltx_denoise step (ltx/e2e_denoise.zig:314 gates it per step). Device
+ * pointer + bytes, valid until the next forward on this context; a stage the
+ * last call did not produce reads NULL / 0. */
 enum {
     LTX_ST_NORM_MSA,    /* s1NormMsa: modulated norm, operand dtype [T][4096] */
     LTX_ST_Q1,          /* normed+roped q times log2(e)/sqrt(128), head-major [32][T][128] (f32 mode: [T][4096], unscaled) */
@@ -138,6 +143,11 @@ enum {
     LTX_ST_X_CA,        /* x after cross-attention [T][4096] f32 */
     LTX_ST_FF_IN,       /* s6FfIn [T][4096] */
     LTX_ST_FF_H,        /* gelu(ff1) [T][16384] */
+    LTX_ST_GLOG2,       /* cross-attention gate logits [T][32] f32 */
+    LTX_ST_Q2,          /* normed cross q times log2(e)/sqrt(128), [32][T][128] (f32 mode: [T][4096], unscaled) */
+    LTX_ST_K2,          /* normed cross k [32][S][128] (f32 mode: [S][4096]) */
+    LTX_ST_V2,          /* cross v: [32][128][S] (f32 mode: [S][4096]) */
+    LTX_ST_VELOCITY,    /* ltx_denoise: the last step's velocity [T][128] f32 */
     LTX_ST_COUNT
 };
 int ltx_block_stage(ltx_ctx* ctx, int stage, void** dev_ptr, uint64_t* bytes);
@@ -146,8 +156,14 @@ int ltx_block_stage(ltx_ctx* ctx, int stage, void** dev_ptr, uint64_t* bytes);
 
 /* y[M][N] = a[M][K] . dq4(q, s)^T (+ bias) with optional GELU-tanh.
  * a: 16-bit [M][K] (mode F16/BF16) or f32 (mode F32); q int8 [N][K];
- * scales [N][K/128] f32 or f16; y f32 (out_f32) or 16-bit. Mirrors linQ
- * (ltx/block.zig:473-477). */
+ * scales [N][K/128] f32 or f16 (f32: finite, magnitude below 2^100, not
+ * checked here); y f32 (out_f32) or 16-bit. Mirrors linQ
+ * (ltx/block.zig:473-477). In the 16-bit modes with N a multiple of 256 the
+ * call first lays the weights out as bytes q + 128 and the scales as words
+ * [K/128][N] in scratch the context owns (allocated on first use, grown as
+ * needed) and then runs the GEMM, all on `stream`: two calls of one context on
+ * different streams may overwrite each other's scratch, so keep one context's
+ * calls on one stream. */
 int ltx_op_linear_q8(ltx_ctx* ctx, const void* a, const int8_t* q, const void* scales, int scale_f16,
                      const float* bias, void* y, int out_f32, int M, int N, int K, int gelu, int mode,
                      void* stream);

@@ -42,7 +42,7 @@ __device__ __forceinline__ void gemm_epilogue(const LtxGemmArgs& a, const f32x16
             const float* gt = nullptr;
             const float* gs = nullptr;
             if (EPI == LTX_EPI_RESID_GATE) {  // ada row of the gate: sst[i] + tstab[tidx[m]][i]
-                gt = a.ada.tstab + ((size_t)a.ada.tidx[m] * 9 + a.igate) * LTX_D;
+                gt = a.ada.tstab + ((size_t)ada_row(a.ada, m) * 9 + a.igate) * LTX_D;
                 gs = a.ada.sst + (size_t)a.igate * LTX_D;
             }
 #pragma unroll
@@ -102,7 +102,7 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
 #pragma unroll
             for (int p = 0; p < RNP; p++) {
                 const int m = min(mb + r0 + RRPP * p, a.M - 1);
-                tix[p] = a.ada.tidx[m];
+                tix[p] = ada_row(a.ada, m);
             }
 #pragma unroll
             for (int p = 0; p < RNP; p++) {

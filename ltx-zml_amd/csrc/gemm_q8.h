@@ -31,8 +31,8 @@
 //   in f32 (exact: at most 19 significant bits), one v_cvt_pk_bf16_f32
 //   rounds a pair (4 per MFMA).
 // - bf16, f32 scales: v_cvt_f32_ubyteN and v_fma_f32 (u, s, -128 s) give
-//   f32(q) * s for scales spanning the whole f32 range, then
-//   v_cvt_pk_bf16_f32 (5 per MFMA).
+//   f32(q) * s, then v_cvt_pk_bf16_f32 (5 per MFMA). -128 s is finite for
+//   |s| < 2^120; uploads refuse f32 scales of magnitude 2^100 or more.
 //
 // LDS layout: A rows of 128 B (8 chunks of 8 k), chunk c of row r stored in
 // slot c ^ ((r >> 1) & 7) (16 consecutive rows, one ds_read_b128 lane group,
@@ -136,7 +136,7 @@ __device__ __forceinline__ bf16x8 q8_dequant8_bf16_f32(uint32_t w0, uint32_t w1,
 }
 
 // bf16 operands, f32 scales: through f32 without a prescaled form, since
-// q * s may span the whole f32 range
+// q * s may reach far beyond the f16 range (|s| < 2^100, as uploads require)
 template <>
 struct Q8Op<__bf16, true> : Q8Mfma<__bf16> {
     typedef Q8ScaleF32 Scale;

@@ -258,6 +258,8 @@ int ltx_denoise(ltx_ctx* c, const ltx_block_weights* const* blocks, int nblocks,
             LtxSchedArgs sa{latent, vel, clean, tk, maskk, tidx, latent, n, LTX_IN_CH, sigma, sigma_next};
             c->launch("ltx_sched_step", (unsigned)((n + 255) / 256), 1, 1, 256, &sa, st);
         }
+        c->stage_ptr[LTX_ST_VELOCITY] = vel;
+        c->stage_bytes[LTX_ST_VELOCITY] = (uint64_t)T * LTX_IN_CH * 4;
     })
 }
 

@@ -97,11 +97,12 @@ static void ensure_ws(ltx_ctx* c, size_t T, size_t S, int mode) {
 
 // ---- launch helpers -------------------------------------------------------
 
-static LtxAda make_ada(const ltx_block_weights* w, const float* tstab, const int32_t* tidx) {
+static LtxAda make_ada(const ltx_block_weights* w, const float* tstab, const int32_t* tidx, int K) {
     LtxAda a;
     a.sst = (const float*)w->sst.p;
     a.tstab = tstab;
     a.tidx = tidx;
+    a.K = K;
     return a;
 }
 
@@ -271,7 +272,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     ensure_ws(c, (size_t)T, (size_t)S, mode);
     std::memset(c->stage_ptr, 0, sizeof(c->stage_ptr));
     const size_t TD = (size_t)T * LTX_D, SD = (size_t)S * LTX_D;
-    LtxAda ada = make_ada(w, tstab, tidx);
+    LtxAda ada = make_ada(w, tstab, tidx, K);
     Carve cv{(char*)c->ws.p, 0, 0, false};
 
     if (mode == LTX_MODE_F32) {
@@ -315,6 +316,10 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
         set_stage(c, LTX_ST_X_CA, b.x_ca, TD * 4);
         set_stage(c, LTX_ST_FF_IN, b.ff_in, TD * 4);
         set_stage(c, LTX_ST_FF_H, b.h, (size_t)T * LTX_FF * 4);
+        set_stage(c, LTX_ST_GLOG2, b.glog2, (size_t)T * LTX_H * 4);
+        set_stage(c, LTX_ST_Q2, b.q2, TD * 4);
+        set_stage(c, LTX_ST_K2, b.k2, SD * 4);
+        set_stage(c, LTX_ST_V2, b.v2, SD * 4);
         return;
     }
 
@@ -394,7 +399,10 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     set_stage(c, LTX_ST_X_CA, b.x_ca, TD * 4);
     set_stage(c, LTX_ST_FF_IN, b.ff_in, TD * 2);
     set_stage(c, LTX_ST_FF_H, b.h, (size_t)T * LTX_FF * 2);
-    (void)SD;
+    set_stage(c, LTX_ST_GLOG2, b.glog2, (size_t)T * LTX_H * 4);
+    set_stage(c, LTX_ST_Q2, b.qh2, TD * 2);
+    set_stage(c, LTX_ST_K2, b.kh2, SD * 2);
+    set_stage(c, LTX_ST_V2, b.vt2, SD * 2);
 }
 
 }  // namespace ltx

@@ -180,8 +180,11 @@ int ltx_blob_open(const char* dir, ltx_blob** out) {
         } catch (const std::exception& ex) {
             fail(ex.what());
         }
-        b->total_bytes = (uint64_t)m.at("total_bytes").as_int();
-        b->align = (uint64_t)m.at("align").as_int();
+        const int64_t total = m.at("total_bytes").as_int(), align = m.at("align").as_int();
+        if (total < 0) fail("BlobSizeMismatch: negative total_bytes");
+        if (align <= 0) fail("Misaligned: manifest align " + std::to_string(align));
+        b->total_bytes = (uint64_t)total;
+        b->align = (uint64_t)align;
         b->block = m.at("block").as_int();
         b->blob_sha = m.at("blob_sha256").as_str();
         for (const auto& e : m.at("entries").arr) {
@@ -189,8 +192,12 @@ int ltx_blob_open(const char* dir, ltx_blob** out) {
             be.name = e.at("name").as_str();
             be.norm = ltx::normalize_name(be.name);
             be.dtype = e.at("dtype").as_str();
-            be.offset = (uint64_t)e.at("offset").as_int();
-            be.nbytes = (uint64_t)e.at("nbytes").as_int();
+            const int64_t off = e.at("offset").as_int(), nb = e.at("nbytes").as_int();
+            // entries lie inside the blob, with no sum that can wrap
+            if (off < 0 || nb < 0 || (uint64_t)nb > b->total_bytes || (uint64_t)off > b->total_bytes - (uint64_t)nb)
+                fail("TrailingBytes: entry beyond the blob: " + be.name);
+            be.offset = (uint64_t)off;
+            be.nbytes = (uint64_t)nb;
             if (const auto* s = e.get("sha256")) be.sha = s->as_str();
             b->entries.push_back(be);
         }

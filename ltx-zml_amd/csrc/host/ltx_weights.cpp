@@ -165,10 +165,32 @@ static uint64_t proj_bytes(const LtxProj& p) {
     return p.q.bytes + p.s.bytes + p.s2.bytes + p.w_bf16.bytes + p.w_f16.bytes + p.bias.bytes;
 }
 
+// f32 scales must be finite and below 2^100 in magnitude: the dequantising
+// GEMMs form q * s as fma(q + 128, s, -128 s), and for fp16 operands from
+// (q + 128) 2^-24 times s 2^24, which stay finite only below that. A scale
+// absmax / 127 of bf16 weights reaches 2^100 only for weights above 1e32.
+static void check_f32_scales(const void* s, size_t n, const char* what) {
+    const uint32_t* u = (const uint32_t*)s;
+    for (size_t i = 0; i < n; i++)
+        if ((u[i] & 0x7fffffffu) >= 0x71800000u)  // |s| >= 2^100, inf or NaN
+            throw Error(std::string("ScaleRange: f32 scale of ") + what + " is not finite or has magnitude >= 2^100");
+}
+
+static void check_scales(const void* const* q8s, const int8_t* const* q8, int sf16) {
+    if (sf16 || !q8 || !q8s) return;
+    for (int qi = 0; qi < LTX_Q_COUNT; qi++) {
+        if (!q8[qi] || !q8s[qi]) continue;
+        int O, I;
+        q_dims(qi, O, I);
+        check_f32_scales(q8s[qi], (size_t)O * (I / LTX_GROUP), kBaseStems[kQBase[qi]]);
+    }
+}
+
 ltx_block_weights* upload(ltx_ctx* c, const void* const* base, const int8_t* const* q8, const void* const* q8s, int sf16) {
     if (!base) throw Error("NULL base weight table");
     for (int i = 0; i < LTX_W_COUNT; i++)
         if (!base[i]) throw Error(std::string("missing base weight ") + kBaseStems[i]);
+    check_scales(q8s, q8, sf16);
     HIPC(hipSetDevice(c->device));
     auto* w = new ltx_block_weights();
     try {
@@ -255,11 +277,20 @@ static BlobLayout parse_layout(uint64_t mem_bytes, const char* manifest, int64_t
     if (!manifest) throw Error("NULL manifest");
     json::Value m = json::parse(manifest);
     check_format_version(m);
+    // alignment of every entry (checkLayout, ltx/loader.zig:56-74); the upload
+    // kernels read entries as 16-byte vectors
+    const json::Value* jal = m.get("align");
+    const int64_t align = jal ? jal->as_int() : 64;
+    if (align <= 0 || align % 16) throw Error("Misaligned: manifest align " + std::to_string(align));
     std::unordered_map<std::string, Entry> ents;
     for (const auto& e : m.at("entries").arr) {
-        Entry en{e.at("dtype").as_str(), (uint64_t)e.at("offset").as_int(), (uint64_t)e.at("nbytes").as_int()};
-        if (en.offset + en.nbytes > mem_bytes) throw Error("manifest entry beyond the blob: " + e.at("name").as_str());
-        ents[normalize_name(e.at("name").as_str())] = en;
+        const std::string& name = e.at("name").as_str();
+        const int64_t off = e.at("offset").as_int(), nb = e.at("nbytes").as_int();
+        // no sum that can wrap: nbytes fits, then offset fits before it
+        if (off < 0 || nb < 0 || (uint64_t)nb > mem_bytes || (uint64_t)off > mem_bytes - (uint64_t)nb)
+            throw Error("manifest entry beyond the blob: " + name);
+        if (off % align) throw Error("Misaligned: " + name);
+        ents[normalize_name(name)] = Entry{e.at("dtype").as_str(), (uint64_t)off, (uint64_t)nb};
     }
     auto find = [&](const std::string& want) -> const Entry* {
         auto it = ents.find(want);
@@ -417,6 +448,13 @@ ltx_block_weights* upload_blob_async(ltx_ctx* c, const void* mem, uint64_t mem_b
                                      int64_t block, ltx_block_weights* reuse, hipStream_t st) {
     if (!mem || !manifest) throw Error("NULL blob or manifest");
     const BlobLayout L = parse_layout(mem_bytes, manifest, block);
+    if (!L.sf16)  // the scale entries are read on the host before the copy
+        for (int qi = 0; qi < LTX_Q_COUNT; qi++)
+            if (L.q8s[qi] >= 0) {
+                int O, I;
+                q_dims(qi, O, I);
+                check_f32_scales((const char*)mem + L.q8s[qi], (size_t)O * (I / LTX_GROUP), kBaseStems[kQBase[qi]]);
+            }
     HIPC(hipSetDevice(c->device));
     if (c->blob_stage.bytes < mem_bytes) c->blob_stage.alloc(mem_bytes);
     // the one DMA of the whole image (asynchronous when `mem` is pinned)

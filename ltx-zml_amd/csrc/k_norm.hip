@@ -20,8 +20,8 @@ __device__ void norm_mod_body(const LtxNormArgs& a) {
     const bool mod = a.isc >= 0;
     bool shared_mod = mod;
     if (mod) {
-        const int r0 = a.ada.tidx[row0];
-        for (int k = 1; k < nr; k++) shared_mod = shared_mod && a.ada.tidx[row0 + k] == r0;
+        const int r0 = ada_row(a.ada, row0);
+        for (int k = 1; k < nr; k++) shared_mod = shared_mod && ada_row(a.ada, row0 + k) == r0;
     }
     float4 sc1[4], sh[4];  // 1 + scale, shift
     auto load_mod = [&](int r) {
@@ -37,7 +37,7 @@ __device__ void norm_mod_body(const LtxNormArgs& a) {
             sh[i] = make_float4(sht.x + shs.x, sht.y + shs.y, sht.z + shs.z, sht.w + shs.w);
         }
     };
-    if (shared_mod) load_mod(a.ada.tidx[row0]);
+    if (shared_mod) load_mod(ada_row(a.ada, row0));
     for (int k = 0; k < nr; k++) {
         const int row = row0 + k;
         const float4* x = (const float4*)(a.x + (size_t)row * LTX_D);
@@ -46,7 +46,7 @@ __device__ void norm_mod_body(const LtxNormArgs& a) {
         for (int i = 0; i < 4; i++) v[i] = x[threadIdx.x + 256 * i];
         // rows with their own timestep row: its modulation rows load before
         // the reduction so their latency overlaps it
-        if (mod && !shared_mod) load_mod(a.ada.tidx[row]);
+        if (mod && !shared_mod) load_mod(ada_row(a.ada, row));
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; i++) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;

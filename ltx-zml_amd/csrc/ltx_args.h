@@ -16,11 +16,14 @@ extern "C" {
 #define LTX_FF 16384
 #define LTX_GROUP 128
 
-// AdaLN gather (ltx/block.zig:47-67): ada_i[t][c] = sst[i][c] + tstab[tidx[t]][i][c].
+// AdaLN gather (ltx/block.zig:47-67): ada_i[t][c] = tstab[row(t)][i][c] + sst[i][c],
+// row(t) = tidx[t] when it lies in 1 .. K-1, else 0 (the reference's select
+// chain starts from row 0 and replaces it only for k = 1 .. K-1).
 typedef struct {
     const float* sst;    // [9][D] per-block table
     const float* tstab;  // [K][9][D] timestep table
     const int32_t* tidx; // [T] row of tstab per token
+    int K;               // rows of tstab
 } LtxAda;
 
 // Fused RMSNorm + AdaLN modulate: y = rms(x) * (1 + ada[isc]) + ada[ish].

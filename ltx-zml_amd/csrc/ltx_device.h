@@ -101,10 +101,17 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
     return (float)__builtin_bit_cast(_Float16, b);
 }
 
-// AdaLN value (ltx/block.zig:47-67): f32 add of the table row and the
-// timestep-table row selected by tidx.
+// The timestep-table row of token t (ltx/block.zig:47-67): tidx[t] when it is
+// in 0 .. K-1, else 0, so no index reads outside the table.
+__device__ __forceinline__ int ada_row(const LtxAda& a, int t) {
+    const int r = a.tidx[t];
+    return (unsigned)r < (unsigned)a.K ? r : 0;
+}
+
+// AdaLN value (ltx/block.zig:47-67): f32 add of the timestep-table row and
+// the table row.
 __device__ __forceinline__ float ada_val(const LtxAda& a, int t, int i, int c) {
-    int r = a.tidx[t];
+    const int r = ada_row(a, t);
     return a.tstab[((size_t)r * 9 + i) * LTX_D + c] + a.sst[(size_t)i * LTX_D + c];
 }
 

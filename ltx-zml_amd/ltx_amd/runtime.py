@@ -20,7 +20,8 @@ MODE_F16, MODE_BF16, MODE_F32 = 0, 1, 2
 ATTN_Q_SCALED = 0x100  # ltx_op_attention mode flag
 ATTN_C = float(np.float32(1.4426950408889634 / 11.313708498984761))  # log2(e) / sqrt(128)
 MODES = {"f16": MODE_F16, "bf16": MODE_BF16, "f32": MODE_F32}
-STAGES = ["norm_msa", "q1", "k1", "v1", "glog1", "attn1", "x_sa", "attn_in", "attn2", "x_ca", "ff_in", "ff_h"]
+STAGES = ["norm_msa", "q1", "k1", "v1", "glog1", "attn1", "x_sa", "attn_in", "attn2", "x_ca", "ff_in", "ff_h",
+          "glog2", "q2", "k2", "v2", "velocity"]
 
 W_COUNT, Q_COUNT = 28, 10
 

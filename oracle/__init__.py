@@ -28,7 +28,7 @@ NF = 682
 MAXPOS = (20.0, 2048.0, 2048.0)
 ST_NAMES = ["s1_norm_msa", "q1_roped", "k1_roped", "v1", "attn1_merged", "s3_attn1", "s4_after_sa", "s4_normed",
             "attn_in", "enc", "q2_normed", "k2_normed", "v2", "attn2_merged", "s5_ca_out", "x_ca", "s6_ff_in",
-            "ff_h", "s7_ff_out"]
+            "ff_h", "s7_ff_out", "glog1", "glog2"]
 BASE_ORDER = ["q1_w", "q1_b", "k1_w", "k1_b", "v1_w", "v1_b", "o1_w", "o1_b", "qn1", "kn1", "g1_w", "g1_b",
               "q2_w", "q2_b", "k2_w", "k2_b", "v2_w", "v2_b", "o2_w", "o2_b", "qn2", "kn2", "g2_w", "g2_b",
               "ff1_w", "ff2_w", "sst", "psst"]
@@ -48,6 +48,9 @@ def lib(real: str = "f64") -> C.CDLL:
     L.orc_block_forward.restype = i32
     L.orc_block_forward.argtypes = [C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), i32, vp, vp, i32, vp, vp, i32, vp,
                                     vp, vp, i32, i32, i32, vp, C.POINTER(vp)]
+    L.orc_block_rows.restype = i32
+    L.orc_block_rows.argtypes = [C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), i32, vp, vp, i32, vp, vp, i32, vp,
+                                 vp, vp, i32, i32, i32, vp, i32, vp, C.POINTER(vp)]
     L.orc_rope_tables.argtypes = [vp, i32, vp, vp]
     L.orc_rope_freqs.argtypes = [vp]
     L.orc_quantize.argtypes = [vp, i32, i32, i32, i32, vp, vp]
@@ -125,9 +128,16 @@ def linear(x, w_bf16=None, q=None, s=None, b_bf16=None, real: str = "f64"):
 
 
 def block_forward(bt, inp: dict, cos_thf: np.ndarray, sin_thf: np.ndarray, chunk: int = 16, cross_chunk: int = 0,
-                  real: str = "f64", stages: bool = False, threads: int | None = None):
+                  real: str = "f64", stages: bool = False, rows=None):
     """QBlock.qBlockOutAll on the CPU. ``bt`` is a BlockTensors (numpy),
-    ``inp`` holds x, ctx, tstab, tidx, pts2; cos/sin in graph layout [T][H][64]."""
+    ``inp`` holds x, ctx, tstab, tidx, pts2; cos/sin in graph layout [T][H][64].
+
+    ``rows``: None for every token, or token indices whose output rows alone
+    are computed (the keys and values of every token are still computed for
+    the self-attention); each returned row equals that row of the whole
+    block. Stage dumps (``stages=True``) then have one row per entry of
+    ``rows``, except k1_roped / v1 (every token) and enc / k2_normed / v2
+    (the S context tokens)."""
     L = lib(real)
     dt = _rdt(real)
     base = (C.c_void_p * 28)(*[bt.base[f].ctypes.data for f in BASE_ORDER])
@@ -141,12 +151,18 @@ def block_forward(bt, inp: dict, cos_thf: np.ndarray, sin_thf: np.ndarray, chunk
         raise ValueError(f"chunk {chunk} does not divide the token count {T}")
     if cross_chunk > 0 and S % cross_chunk:
         raise ValueError(f"cross_chunk {cross_chunk} does not divide the context length {S}")
-    out = np.empty((T, D), dt)
+    if rows is not None:
+        rows = np.ascontiguousarray(rows, np.int32)
+        if rows.ndim != 1 or rows.size == 0 or rows.min() < 0 or rows.max() >= T:
+            raise ValueError("rows must be a non-empty list of token indices")
+    nr = T if rows is None else rows.size
+    out = np.empty((nr, D), dt)
     st_bufs = {}
     st_arr = None
     if stages:
-        shapes = {"ff_h": (T, FF), "enc": (S, D), "k2_normed": (S, D), "v2": (S, D)}
-        st_bufs = {n: np.empty(shapes.get(n, (T, D)), dt) for n in ST_NAMES}
+        shapes = {"ff_h": (nr, FF), "enc": (S, D), "k2_normed": (S, D), "v2": (S, D), "k1_roped": (T, D),
+                  "v1": (T, D), "glog1": (nr, H), "glog2": (nr, H)}
+        st_bufs = {n: np.empty(shapes.get(n, (nr, D)), dt) for n in ST_NAMES}
         st_arr = (C.c_void_p * len(ST_NAMES))(*[st_bufs[n].ctypes.data for n in ST_NAMES])
     tstab = np.ascontiguousarray(inp["tstab"], np.float32)
     tidx = np.ascontiguousarray(inp["tidx"], np.int32)
@@ -154,9 +170,12 @@ def block_forward(bt, inp: dict, cos_thf: np.ndarray, sin_thf: np.ndarray, chunk
     pts2 = np.ascontiguousarray(inp["pts2"], np.float32)
     cos_thf = np.ascontiguousarray(cos_thf, np.float32)
     sin_thf = np.ascontiguousarray(sin_thf, np.float32)
-    ok = L.orc_block_forward(base, q8, q8s, int(bt.scale_f16), x.ctypes.data, tstab.ctypes.data, tstab.shape[0],
-                             tidx.ctypes.data, ctx.ctypes.data, S, pts2.ctypes.data, cos_thf.ctypes.data,
-                             sin_thf.ctypes.data, T, chunk, cross_chunk, out.ctypes.data, st_arr)
+    args = (base, q8, q8s, int(bt.scale_f16), x.ctypes.data, tstab.ctypes.data, tstab.shape[0], tidx.ctypes.data,
+            ctx.ctypes.data, S, pts2.ctypes.data, cos_thf.ctypes.data, sin_thf.ctypes.data, T, chunk, cross_chunk)
+    if rows is None:
+        ok = L.orc_block_forward(*args, out.ctypes.data, st_arr)
+    else:
+        ok = L.orc_block_rows(*args, rows.ctypes.data, nr, out.ctypes.data, st_arr)
     if not ok:
         raise RuntimeError("oracle block forward failed")
     return (out, st_bufs) if stages else out
@@ -214,19 +233,35 @@ def _bf(b):
     return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
+_W_CACHE: dict = {}
+
+
+def _weights_np(bt) -> dict:
+    """f64 weights of a block (dq4 of the int8 companions, else bf16),
+    cached by the identity of the tensors they come from."""
+    key = tuple(id(bt.base[f]) for f in BASE_ORDER[:-2]) + tuple(id(a) for a in bt.q8.values())
+    if key not in _W_CACHE:
+        W = {}
+        for f in BASE_ORDER[:-2]:
+            W[f] = _bf(bt.base[f])
+        for n, wf in {"q1": "q1_w", "k1": "k1_w", "v1": "v1_w", "q2": "q2_w", "k2": "k2_w", "v2": "v2_w",
+                      "f1": "ff1_w", "f2": "ff2_w", "o1": "o1_w", "o2": "o2_w"}.items():
+            if n in bt.q8:
+                q = bt.q8[n].astype(np.float32)
+                s = bt.q8s[n].astype(np.float32)
+                W[wf] = (q.reshape(q.shape[0], -1, 128) * s[:, :, None]).reshape(q.shape).astype(np.float64)
+        _W_CACHE.clear()
+        _W_CACHE[key] = (W, (bt.base, bt.q8))  # the tensors stay referenced while cached
+    return _W_CACHE[key][0]
+
+
 def block_np(bt, inp: dict, cos_thf, sin_thf, mistake: str | None = None):
     """Dense-attention numpy restatement of qBlockOutAll (f64). `mistake`
     plants one deliberate error (tests use it to show the gates have teeth):
-    layernorm | gate_no_2x | rope_sign | kv_scale | ada_swap."""
-    W = {}
-    for f in BASE_ORDER[:-2]:
-        W[f] = _bf(bt.base[f])
-    for n, wf in {"q1": "q1_w", "k1": "k1_w", "v1": "v1_w", "q2": "q2_w", "k2": "k2_w", "v2": "v2_w",
-                  "f1": "ff1_w", "f2": "ff2_w", "o1": "o1_w", "o2": "o2_w"}.items():
-        if n in bt.q8:
-            q = bt.q8[n].astype(np.float32)
-            s = bt.q8s[n].astype(np.float32)
-            W[wf] = (q.reshape(q.shape[0], -1, 128) * s[:, :, None]).reshape(q.shape).astype(np.float64)
+    layernorm | gate_no_2x | rope_sign | kv_scale | ada_swap (self-attention
+    shift and scale rows exchanged) | ca_swap (cross-attention query rows) |
+    ff_swap (FFN rows) | kv_swap (the K/V modulation rows)."""
+    W = dict(_weights_np(bt))
     sst = bt.base["sst"].astype(np.float64)
     psst = bt.base["psst"].astype(np.float64)
     x = inp["x"].astype(np.float64)
@@ -267,12 +302,16 @@ def block_np(bt, inp: dict, cos_thf, sin_thf, mistake: str | None = None):
             W2[f"a{a}{t}_w"] = W[f"{t}{a}_w"]
             W2[f"a{a}{t}_b"] = W[f"{t}{a}_b"]
     W.update(W2)
-    if mistake == "ada_swap":  # shift and scale rows exchanged
-        ada[0], ada[1] = ada[1], ada[0]
+    swaps = {"ada_swap": (0, 1), "ca_swap": (6, 7), "ff_swap": (3, 4)}
+    if mistake in swaps:  # shift and scale rows exchanged
+        i, j = swaps[mistake]
+        ada[i], ada[j] = ada[j], ada[i]
     n = rms(x) * (1 + ada[1]) + ada[0]
     x_sa = x + attn(n, n, "a1", True) * ada[2]
     ai = rms(x_sa) * (1 + ada[7]) + ada[6]
     kv = psst + inp["pts2"].astype(np.float64)
+    if mistake == "kv_swap":
+        kv = kv[::-1]
     enc = ctx * (kv[1] if mistake == "kv_scale" else 1 + kv[1]) + kv[0]
     x_ca = x_sa + attn(ai, enc, "a2", False) * ada[8]
     fi = rms(x_ca) * (1 + ada[4]) + ada[3]

@@ -17,9 +17,9 @@ def build(verbose: bool = False) -> None:
     OUT.mkdir(exist_ok=True)
     src = str(HERE / "ltx_oracle.c")
     cmds = [
-        ["gcc", "-O2", "-fopenmp", "-fPIC", "-shared", "-ffp-contract=off", "-DREAL=double", src,
+        ["gcc", "-O3", "-fopenmp", "-fPIC", "-shared", "-march=x86-64-v3", "-ffp-contract=off", "-DREAL=double", src,
          "-o", str(OUT / "liboracle_f64.so"), "-lm"],
-        ["gcc", "-O3", "-fopenmp", "-fPIC", "-shared", "-march=x86-64-v3", "-DREAL=float", src,
+        ["gcc", "-O3", "-fopenmp", "-fPIC", "-shared", "-march=x86-64-v3", "-DREAL=float", "-DREAL_F32", src,
          "-o", str(OUT / "liboracle_f32.so"), "-lm"],
     ]
     for c in cmds:

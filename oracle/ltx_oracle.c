@@ -149,27 +149,99 @@ void orc_rope_tables(const float* grid, int T, float* cos_out, float* sin_out) {
 
 /* ---- dense linear algebra ---------------------------------------------- */
 
-/* C[M][N] = A[M][K] * Bt[K][N]; saxpy form, sequential k order per output. */
-static void gemm_kn(const real* A, int M, int K, const real* Bt, int N, real* C) {
-    enum { MB = 4, NB = 64 };
-    int nnb = (N + NB - 1) / NB;
-#pragma omp parallel for schedule(dynamic, 1)
-    for (int nb = 0; nb < nnb; nb++) {
-        int n0 = nb * NB, nn = N - n0 < NB ? N - n0 : NB;
-        for (int m0 = 0; m0 < M; m0 += MB) {
-            int mm = M - m0 < MB ? M - m0 : MB;
-            real acc[MB][NB];
-            memset(acc, 0, sizeof(acc));
-            for (int k = 0; k < K; k++) {
-                const real* b = Bt + (size_t)k * N + n0;
-                for (int i = 0; i < mm; i++) {
-                    real a = A[(size_t)(m0 + i) * K + k];
-                    for (int j = 0; j < nn; j++) acc[i][j] += a * b[j];
-                }
-            }
-            for (int i = 0; i < mm; i++)
-                for (int j = 0; j < nn; j++) C[(size_t)(m0 + i) * N + n0 + j] = acc[i][j];
+/* C[M][N] = A[M][K] * Bt[K][N]. Every output is one chain of fused
+ * multiply-adds over k in ascending order (the accumulator goes to C and back
+ * between k-blocks, which does not change the chain), so a row's result does
+ * not depend on the blocking or on which other rows are computed with it.
+ * Blocked for the caches: k-blocks of KC, micro-tiles of MR x NR outputs
+ * held in registers. */
+#include <immintrin.h>
+#ifdef REAL_F32
+typedef __m256 vreal;
+#define VW 8
+#define V_LOAD _mm256_loadu_ps
+#define V_STORE _mm256_storeu_ps
+#define V_BCAST _mm256_broadcast_ss
+#define V_FMA _mm256_fmadd_ps
+#else
+typedef __m256d vreal;
+#define VW 4
+#define V_LOAD _mm256_loadu_pd
+#define V_STORE _mm256_storeu_pd
+#define V_BCAST _mm256_broadcast_sd
+#define V_FMA _mm256_fmadd_pd
+#endif
+#define MR 6
+#define NR (2 * VW)
+#define KC 256
+#define MC 48
+#define NC 256
+
+static inline real fma_r(real a, real b, real c) {
+    return sizeof(real) == sizeof(double) ? (real)__builtin_fma((double)a, (double)b, (double)c)
+                                          : (real)__builtin_fmaf((float)a, (float)b, (float)c);
+}
+
+/* A full MR x NR tile: twelve vector accumulators, one broadcast of A per
+ * row and k (vfmadd: one rounding, as fma_r). */
+static inline void gemm_micro_full(const real* A, int lda, const real* B, int ldb, real* C, int ldc, int kc) {
+#define ROW_LOAD(i) vreal c##i##0 = V_LOAD(C + (size_t)(i) * ldc), c##i##1 = V_LOAD(C + (size_t)(i) * ldc + VW);
+#define ROW_FMA(i)                                              \
+    {                                                           \
+        const vreal a = V_BCAST(A + (size_t)(i) * lda + k);     \
+        c##i##0 = V_FMA(a, b0, c##i##0);                        \
+        c##i##1 = V_FMA(a, b1, c##i##1);                        \
+    }
+#define ROW_STORE(i)                                  \
+    V_STORE(C + (size_t)(i) * ldc, c##i##0);          \
+    V_STORE(C + (size_t)(i) * ldc + VW, c##i##1);
+    ROW_LOAD(0) ROW_LOAD(1) ROW_LOAD(2) ROW_LOAD(3) ROW_LOAD(4) ROW_LOAD(5)
+    for (int k = 0; k < kc; k++) {
+        const vreal b0 = V_LOAD(B + (size_t)k * ldb), b1 = V_LOAD(B + (size_t)k * ldb + VW);
+        ROW_FMA(0) ROW_FMA(1) ROW_FMA(2) ROW_FMA(3) ROW_FMA(4) ROW_FMA(5)
+    }
+    ROW_STORE(0) ROW_STORE(1) ROW_STORE(2) ROW_STORE(3) ROW_STORE(4) ROW_STORE(5)
+#undef ROW_LOAD
+#undef ROW_FMA
+#undef ROW_STORE
+}
+
+static inline void gemm_micro(const real* A, int lda, const real* B, int ldb, real* C, int ldc, int mr, int nr,
+                              int kc) {
+    if (mr == MR && nr == NR) {
+        gemm_micro_full(A, lda, B, ldb, C, ldc, kc);
+        return;
+    }
+    real acc[MR][NR];
+    for (int i = 0; i < mr; i++)
+        for (int j = 0; j < nr; j++) acc[i][j] = C[(size_t)i * ldc + j];
+    for (int k = 0; k < kc; k++) {
+        const real* b = B + (size_t)k * ldb;
+        for (int i = 0; i < mr; i++) {
+            const real a = A[(size_t)i * lda + k];
+            for (int j = 0; j < nr; j++) acc[i][j] = fma_r(a, b[j], acc[i][j]);
         }
+    }
+    for (int i = 0; i < mr; i++)
+        for (int j = 0; j < nr; j++) C[(size_t)i * ldc + j] = acc[i][j];
+}
+
+static void gemm_kn(const real* A, int M, int K, const real* Bt, int N, real* C) {
+    const int nmb = (M + MC - 1) / MC, nnb = (N + NC - 1) / NC;
+#pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; m++) memset(C + (size_t)m * N, 0, sizeof(real) * (size_t)N);
+    for (int k0 = 0; k0 < K; k0 += KC) {
+        const int kc = K - k0 < KC ? K - k0 : KC;
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+        for (int nb = 0; nb < nnb; nb++)
+            for (int mb = 0; mb < nmb; mb++) {
+                const int n0 = nb * NC, m0 = mb * MC;
+                const int n1 = N < n0 + NC ? N : n0 + NC, m1 = M < m0 + MC ? M : m0 + MC;
+                for (int n = n0; n < n1; n += NR)
+                    for (int m = m0; m < m1; m += MR)
+                        gemm_micro(A + (size_t)m * K + k0, K, Bt + (size_t)k0 * N + n, N, C + (size_t)m * N + n, N,
+                                   m1 - m < MR ? m1 - m : MR, n1 - n < NR ? n1 - n : NR, kc);
+            }
     }
 }
 
@@ -177,19 +249,25 @@ static void gemm_kn(const real* A, int M, int K, const real* Bt, int N, real* C)
  * scale [N][K/128] pair (dq4 semantics: f32(q)*s rounded once to f32). */
 static real* weight_t(const uint16_t* wbf, const int8_t* q, const void* s, int scale_f16, int N, int K) {
     real* wt = (real*)malloc(sizeof(real) * (size_t)N * K);
-    int G = K / 128;
-#pragma omp parallel for schedule(static)
-    for (int n = 0; n < N; n++)
-        for (int k = 0; k < K; k++) {
-            real v;
-            if (q) {
-                float sc = scale_f16 ? f16_to_f32(((const uint16_t*)s)[(size_t)n * G + k / 128])
-                                     : ((const float*)s)[(size_t)n * G + k / 128];
-                v = (real)((float)q[(size_t)n * K + k] * sc);
-            } else {
-                v = bfr(wbf, (size_t)n * K + k);
-            }
-            wt[(size_t)k * N + n] = v;
+    const int G = K / 128, TB = 64;
+    const int ntn = (N + TB - 1) / TB, ntk = (K + TB - 1) / TB;
+    /* 64 x 64 tiles, so the transposed stores stay within a few cache lines */
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int tn = 0; tn < ntn; tn++)
+        for (int tk = 0; tk < ntk; tk++) {
+            const int n1 = N < (tn + 1) * TB ? N : (tn + 1) * TB, k1 = K < (tk + 1) * TB ? K : (tk + 1) * TB;
+            for (int n = tn * TB; n < n1; n++)
+                for (int k = tk * TB; k < k1; k++) {
+                    real v;
+                    if (q) {
+                        float sc = scale_f16 ? f16_to_f32(((const uint16_t*)s)[(size_t)n * G + k / 128])
+                                             : ((const float*)s)[(size_t)n * G + k / 128];
+                        v = (real)((float)q[(size_t)n * K + k] * sc);
+                    } else {
+                        v = bfr(wbf, (size_t)n * K + k);
+                    }
+                    wt[(size_t)k * N + n] = v;
+                }
         }
     return wt;
 }
@@ -223,20 +301,32 @@ static void rms_rows(const real* x, int M, int N, const uint16_t* w, real* y) {
     }
 }
 
-/* adaVal (ltx/block.zig:47-67): ada_i[t] = sst[i] + tstab[tidx[t], i] */
-static inline real ada(const float* sst, const float* tstab, const int32_t* tidx, int t, int i, int c) {
-    return (real)tstab[((size_t)tidx[t] * 9 + i) * D + c] + (real)sst[(size_t)i * D + c];
+/* adaVal (ltx/block.zig:47-67): ada_i[t] = tstab[row(t), i] + sst[i]. The
+ * reference selects the row with a chain over k = 1 .. K-1 starting from row
+ * 0, so an index outside 1 .. K-1 takes row 0 (ada_rows resolves that once
+ * per token; `trow` below holds the resolved rows). */
+static int32_t* ada_rows(const int32_t* tidx, const int* rows, int n, int K) {
+    int32_t* r = (int32_t*)malloc(sizeof(int32_t) * (size_t)(n > 0 ? n : 1));
+    for (int i = 0; i < n; i++) {
+        const int32_t k = tidx[rows ? rows[i] : i];
+        r[i] = (k >= 1 && k < K) ? k : 0;
+    }
+    return r;
+}
+
+static inline real ada(const float* sst, const float* tstab, const int32_t* trow, int t, int i, int c) {
+    return (real)tstab[((size_t)trow[t] * 9 + i) * D + c] + (real)sst[(size_t)i * D + c];
 }
 
 /* modulate(rms(x), ada[isc], ada[ish]) (ltx/block.zig:36-38, 248-252) */
-static void norm_mod(const real* x, int T, const float* sst, const float* tstab, const int32_t* tidx,
+static void norm_mod(const real* x, int T, const float* sst, const float* tstab, const int32_t* trow,
                      int ish, int isc, real* y) {
     rms_rows(x, T, D, NULL, y);
 #pragma omp parallel for schedule(static)
     for (int t = 0; t < T; t++)
         for (int c = 0; c < D; c++) {
             real n = y[(size_t)t * D + c];
-            y[(size_t)t * D + c] = n * (ada(sst, tstab, tidx, t, isc, c) + 1) + ada(sst, tstab, tidx, t, ish, c);
+            y[(size_t)t * D + c] = n * (ada(sst, tstab, trow, t, isc, c) + 1) + ada(sst, tstab, trow, t, ish, c);
         }
 }
 
@@ -349,11 +439,11 @@ enum {
 /* Quantized companions (ltx/loader.zig:147-156, plus the out-projections). */
 enum { Q_Q1, Q_K1, Q_V1, Q_Q2, Q_K2, Q_V2, Q_F1, Q_F2, Q_O1, Q_O2, Q_COUNT };
 
-/* Stage dumps, in forward order. */
+/* Stage dumps, in forward order (glog1 / glog2, the gate logits, last). */
 enum {
     ST_S1_NORM_MSA, ST_Q1_ROPED, ST_K1_ROPED, ST_V1, ST_ATTN1_MERGED, ST_S3_ATTN1, ST_S4_AFTER_SA,
     ST_S4_NORMED, ST_ATTN_IN, ST_ENC, ST_Q2_NORMED, ST_K2_NORMED, ST_V2, ST_ATTN2_MERGED, ST_S5_CA_OUT,
-    ST_X_CA, ST_S6_FF_IN, ST_FF_H, ST_S7_FF_OUT, ST_COUNT
+    ST_X_CA, ST_S6_FF_IN, ST_FF_H, ST_S7_FF_OUT, ST_GLOG1, ST_GLOG2, ST_COUNT
 };
 
 static void dump(real* const* stages, int id, const real* src, size_t n) {
@@ -365,43 +455,47 @@ static void dump(real* const* stages, int id, const real* src, size_t n) {
 #define QS(i) (q8s ? q8s[i] : NULL)
 
 /* One attention (Block.attention, ltx/block.zig:212-244 / QBlock,
- * ltx/block.zig:500-530, 557-567): q = rmsW(lin(x)), k = rmsW(lin(ctx)),
- * v = lin(ctx), optional RoPE, sdpa, gate 2*sigmoid(lin(x, gw, gb)) per
- * (token, head) from the attention input, merge heads, output projection.
- * Weight slot ids: qi/ki/vi/oi index both base (bf16) and q8 tables. */
+ * ltx/block.zig:500-530, 557-567): q = rmsW(lin(xq)), k = rmsW(lin(xkv)),
+ * v = lin(xkv), RoPE on q and k when tables are given (rows of q and k each
+ * with their own [rows][H][64] tables), sdpa, gate 2*sigmoid(lin(xq, gw, gb))
+ * per (token, head) from the attention input, merge heads, output
+ * projection. Every op but the sdpa is row-local, so xq may be any subset of
+ * the query rows. Weight slot ids index both base (bf16) and q8 tables. */
 static void attention(const void* const* base, const int8_t* const* q8, const void* const* q8s, int sf16,
-                      const real* x, int T, const real* ctxv, int S, int bq, int bk, int bv, int bo, int iqn,
-                      int ikn, int igw, int qq, int qk, int qv, int qo, const float* cs, const float* sn,
-                      int chunk, real* out, real* const* stages, int st_q, int st_k, int st_v, int st_merged) {
-    real* q = (real*)malloc(sizeof(real) * (size_t)T * D);
+                      const real* xq, int Tq, const float* csq, const float* snq, const real* xkv, int S,
+                      const float* cskv, const float* snkv, int bq, int bk, int bv, int bo, int iqn, int ikn, int igw,
+                      int qq, int qk, int qv, int qo, int chunk, real* out, real* const* stages, int st_q, int st_k,
+                      int st_v, int st_merged, int st_glog) {
+    real* q = (real*)malloc(sizeof(real) * (size_t)Tq * D);
     real* k = (real*)malloc(sizeof(real) * (size_t)S * D);
     real* v = (real*)malloc(sizeof(real) * (size_t)S * D);
-    real* o = (real*)malloc(sizeof(real) * (size_t)T * D);
-    linear(x, T, D, BW(bq), QW(qq), QS(qq), sf16, BW(bq + 1), D, q);
-    rms_rows(q, T, D, BW(iqn), q);
-    linear(ctxv, S, D, BW(bk), QW(qk), QS(qk), sf16, BW(bk + 1), D, k);
+    real* o = (real*)malloc(sizeof(real) * (size_t)Tq * D);
+    linear(xq, Tq, D, BW(bq), QW(qq), QS(qq), sf16, BW(bq + 1), D, q);
+    rms_rows(q, Tq, D, BW(iqn), q);
+    linear(xkv, S, D, BW(bk), QW(qk), QS(qk), sf16, BW(bk + 1), D, k);
     rms_rows(k, S, D, BW(ikn), k);
-    linear(ctxv, S, D, BW(bv), QW(qv), QS(qv), sf16, BW(bv + 1), D, v);
-    if (cs) {
-        rope_apply(q, T, cs, sn);
-        rope_apply(k, S, cs, sn);
+    linear(xkv, S, D, BW(bv), QW(qv), QS(qv), sf16, BW(bv + 1), D, v);
+    if (csq) {
+        rope_apply(q, Tq, csq, snq);
+        rope_apply(k, S, cskv, snkv);
     }
-    dump(stages, st_q, q, (size_t)T * D);
+    dump(stages, st_q, q, (size_t)Tq * D);
     dump(stages, st_k, k, (size_t)S * D);
     dump(stages, st_v, v, (size_t)S * D);
-    if (!orc_sdpa(q, T, k, v, S, chunk, o)) { /* chunk must divide the key count */
-        memset(o, 0xff, sizeof(real) * (size_t)T * D); /* NaN: fails loudly */
+    if (!orc_sdpa(q, Tq, k, v, S, chunk, o)) { /* chunk must divide the key count */
+        memset(o, 0xff, sizeof(real) * (size_t)Tq * D); /* NaN: fails loudly */
     }
-    real* glog = (real*)malloc(sizeof(real) * (size_t)T * H);
-    linear(x, T, D, BW(igw), NULL, NULL, 0, BW(igw + 1), H, glog);
+    real* glog = (real*)malloc(sizeof(real) * (size_t)Tq * H);
+    linear(xq, Tq, D, BW(igw), NULL, NULL, 0, BW(igw + 1), H, glog);
+    dump(stages, st_glog, glog, (size_t)Tq * H);
 #pragma omp parallel for schedule(static)
-    for (int t = 0; t < T; t++)
+    for (int t = 0; t < Tq; t++)
         for (int h = 0; h < H; h++) {
             real g = sigmoid_r(glog[(size_t)t * H + h]) * 2;
             for (int e = 0; e < HD; e++) o[(size_t)t * D + h * HD + e] *= g;
         }
-    dump(stages, st_merged, o, (size_t)T * D);
-    linear(o, T, D, BW(bo), QW(qo), QS(qo), sf16, BW(bo + 1), D, out);
+    dump(stages, st_merged, o, (size_t)Tq * D);
+    linear(o, Tq, D, BW(bo), QW(qo), QS(qo), sf16, BW(bo + 1), D, out);
     free(glog);
     free(q);
     free(k);
@@ -409,46 +503,83 @@ static void attention(const void* const* base, const int8_t* const* q8, const vo
     free(o);
 }
 
+/* Rows `rows[0 .. nr)` of a [T][w] table (every row when rows is NULL). */
+static float* gather_f32(const float* src, const int* rows, int nr, size_t w) {
+    float* d = (float*)malloc(sizeof(float) * (size_t)nr * w);
+    for (int i = 0; i < nr; i++) memcpy(d + (size_t)i * w, src + (size_t)rows[i] * w, sizeof(float) * w);
+    return d;
+}
+
 /* QBlock.qBlockOutAll (ltx/block.zig:544-574) with the self-attention
  * computed blockwise (chunk) — the production attention algorithm
  * (ltx/block.zig:105-154); cross-attention dense (cross_chunk 0) as in the
- * reference, or blockwise. q8[i] == NULL selects the bf16 base weight. */
-int orc_block_forward(const void* const* base, const int8_t* const* q8, const void* const* q8s, int scale_f16,
-                      const float* x_in, const float* tstab, int K, const int32_t* tidx, const float* ctx_in,
-                      int S, const float* pts2, const float* cs, const float* sn, int T, int chunk,
-                      int cross_chunk, real* out, real* const* stages) {
-    (void)K;
+ * reference, or blockwise. q8[i] == NULL selects the bf16 base weight.
+ *
+ * Output rows: all T tokens (rows == NULL), or only the tokens rows[0 .. nr)
+ * (out is [nr][D]). Every op except the self-attention is token-local, so a
+ * subset computes the modulated norm, K and V of every token (the keys) and
+ * everything else for its own rows only; each of its rows equals that row of
+ * the whole block (the same operations in the same order). Stage dumps
+ * follow the computed rows: K1 / V1 have T rows, ENC / K2 / V2 have S, the
+ * rest nr. */
+static int block_rows(const void* const* base, const int8_t* const* q8, const void* const* q8s, int scale_f16,
+                      const float* x_in, const float* tstab, int K, const int32_t* tidx, const float* ctx_in, int S,
+                      const float* pts2, const float* cs, const float* sn, int T, int chunk, int cross_chunk,
+                      const int* rows, int nr, real* out, real* const* stages) {
+    if (K <= 0 || T <= 0 || S <= 0) return 0;
+    if (rows) {
+        if (nr <= 0) return 0;
+        for (int i = 0; i < nr; i++)
+            if (rows[i] < 0 || rows[i] >= T) return 0;
+    } else {
+        nr = T;
+    }
     const float* sst = (const float*)base[W_SST];
     const float* psst = (const float*)base[W_PSST];
-    size_t TD = (size_t)T * D;
-    real* x = (real*)malloc(sizeof(real) * TD);
-    real* n = (real*)malloc(sizeof(real) * TD);
-    real* a = (real*)malloc(sizeof(real) * TD);
-    real* x_sa = (real*)malloc(sizeof(real) * TD);
-    for (size_t i = 0; i < TD; i++) x[i] = x_in[i];
-
-    /* self-attention: n = modulate(rms(x), ada1, ada0) */
-    norm_mod(x, T, sst, tstab, tidx, 0, 1, n);
-    dump(stages, ST_S1_NORM_MSA, n, TD);
-    attention(base, q8, q8s, scale_f16, n, T, n, T, W_Q1_W, W_K1_W, W_V1_W, W_O1_W, W_QN1, W_KN1, W_G1_W, Q_Q1,
-              Q_K1, Q_V1, Q_O1, cs, sn, chunk, a, stages, ST_Q1_ROPED, ST_K1_ROPED, ST_V1, ST_ATTN1_MERGED);
-    dump(stages, ST_S3_ATTN1, a, TD);
+    const size_t TD = (size_t)T * D, RD = (size_t)nr * D;
+    int32_t* trow_all = ada_rows(tidx, NULL, T, K);
+    int32_t* trow = rows ? ada_rows(tidx, rows, nr, K) : trow_all;
+    real* x = (real*)malloc(sizeof(real) * RD);  /* the output rows' x, later x_ca */
+    real* n_all = (real*)malloc(sizeof(real) * TD);
+    real* a = (real*)malloc(sizeof(real) * RD);
+    real* x_sa = (real*)malloc(sizeof(real) * RD);
+    {
+        real* x_all = (real*)malloc(sizeof(real) * TD);
+        for (size_t i = 0; i < TD; i++) x_all[i] = x_in[i];
+        /* self-attention: n = modulate(rms(x), ada1, ada0), for every token */
+        norm_mod(x_all, T, sst, tstab, trow_all, 0, 1, n_all);
+        for (int i = 0; i < nr; i++)
+            memcpy(x + (size_t)i * D, x_all + (size_t)(rows ? rows[i] : i) * D, sizeof(real) * D);
+        free(x_all);
+    }
+    real* n = (real*)malloc(sizeof(real) * RD);  /* the output rows' modulated norm */
+    for (int i = 0; i < nr; i++) memcpy(n + (size_t)i * D, n_all + (size_t)(rows ? rows[i] : i) * D, sizeof(real) * D);
+    dump(stages, ST_S1_NORM_MSA, n, RD);
+    float* csq = rows ? gather_f32(cs, rows, nr, (size_t)H * 64) : NULL;
+    float* snq = rows ? gather_f32(sn, rows, nr, (size_t)H * 64) : NULL;
+    attention(base, q8, q8s, scale_f16, n, nr, rows ? csq : cs, rows ? snq : sn, n_all, T, cs, sn, W_Q1_W, W_K1_W,
+              W_V1_W, W_O1_W, W_QN1, W_KN1, W_G1_W, Q_Q1, Q_K1, Q_V1, Q_O1, chunk, a, stages, ST_Q1_ROPED,
+              ST_K1_ROPED, ST_V1, ST_ATTN1_MERGED, ST_GLOG1);
+    free(csq);
+    free(snq);
+    free(n_all);
+    dump(stages, ST_S3_ATTN1, a, RD);
 #pragma omp parallel for schedule(static)
-    for (int t = 0; t < T; t++)
+    for (int t = 0; t < nr; t++)
         for (int c = 0; c < D; c++)
-            x_sa[(size_t)t * D + c] = x[(size_t)t * D + c] + a[(size_t)t * D + c] * ada(sst, tstab, tidx, t, 2, c);
-    dump(stages, ST_S4_AFTER_SA, x_sa, TD);
+            x_sa[(size_t)t * D + c] = x[(size_t)t * D + c] + a[(size_t)t * D + c] * ada(sst, tstab, trow, t, 2, c);
+    dump(stages, ST_S4_AFTER_SA, x_sa, RD);
 
     /* cross-attention (ltx/block.zig:548-568) */
-    rms_rows(x_sa, T, D, NULL, n);
-    dump(stages, ST_S4_NORMED, n, TD);
+    rms_rows(x_sa, nr, D, NULL, n);
+    dump(stages, ST_S4_NORMED, n, RD);
 #pragma omp parallel for schedule(static)
-    for (int t = 0; t < T; t++)
+    for (int t = 0; t < nr; t++)
         for (int c = 0; c < D; c++) {
             real v = n[(size_t)t * D + c];
-            n[(size_t)t * D + c] = v * (ada(sst, tstab, tidx, t, 7, c) + 1) + ada(sst, tstab, tidx, t, 6, c);
+            n[(size_t)t * D + c] = v * (ada(sst, tstab, trow, t, 7, c) + 1) + ada(sst, tstab, trow, t, 6, c);
         }
-    dump(stages, ST_ATTN_IN, n, TD);
+    dump(stages, ST_ATTN_IN, n, RD);
     real* enc = (real*)malloc(sizeof(real) * (size_t)S * D);
     for (int t = 0; t < S; t++)
         for (int c = 0; c < D; c++) {
@@ -457,38 +588,60 @@ int orc_block_forward(const void* const* base, const int8_t* const* q8, const vo
             enc[(size_t)t * D + c] = (real)ctx_in[(size_t)t * D + c] * (sc + 1) + sh;
         }
     dump(stages, ST_ENC, enc, (size_t)S * D);
-    attention(base, q8, q8s, scale_f16, n, T, enc, S, W_Q2_W, W_K2_W, W_V2_W, W_O2_W, W_QN2, W_KN2, W_G2_W, Q_Q2,
-              Q_K2, Q_V2, Q_O2, NULL, NULL, cross_chunk, a, stages, ST_Q2_NORMED, ST_K2_NORMED, ST_V2,
-              ST_ATTN2_MERGED);
+    attention(base, q8, q8s, scale_f16, n, nr, NULL, NULL, enc, S, NULL, NULL, W_Q2_W, W_K2_W, W_V2_W, W_O2_W, W_QN2,
+              W_KN2, W_G2_W, Q_Q2, Q_K2, Q_V2, Q_O2, cross_chunk, a, stages, ST_Q2_NORMED, ST_K2_NORMED, ST_V2,
+              ST_ATTN2_MERGED, ST_GLOG2);
     free(enc);
 #pragma omp parallel for schedule(static)
-    for (int t = 0; t < T; t++)
-        for (int c = 0; c < D; c++) a[(size_t)t * D + c] *= ada(sst, tstab, tidx, t, 8, c);
-    dump(stages, ST_S5_CA_OUT, a, TD);
+    for (int t = 0; t < nr; t++)
+        for (int c = 0; c < D; c++) a[(size_t)t * D + c] *= ada(sst, tstab, trow, t, 8, c);
+    dump(stages, ST_S5_CA_OUT, a, RD);
     real* x_ca = x; /* reuse */
-    for (size_t i = 0; i < TD; i++) x_ca[i] = x_sa[i] + a[i];
-    dump(stages, ST_X_CA, x_ca, TD);
+    for (size_t i = 0; i < RD; i++) x_ca[i] = x_sa[i] + a[i];
+    dump(stages, ST_X_CA, x_ca, RD);
 
     /* feed-forward (ltx/block.zig:569-573, qFf 532-534) */
-    norm_mod(x_ca, T, sst, tstab, tidx, 3, 4, n);
-    dump(stages, ST_S6_FF_IN, n, TD);
-    real* h = (real*)malloc(sizeof(real) * (size_t)T * FF);
-    linear(n, T, D, BW(W_FF1_W), QW(Q_F1), QS(Q_F1), scale_f16, NULL, FF, h);
+    norm_mod(x_ca, nr, sst, tstab, trow, 3, 4, n);
+    dump(stages, ST_S6_FF_IN, n, RD);
+    real* h = (real*)malloc(sizeof(real) * (size_t)nr * FF);
+    linear(n, nr, D, BW(W_FF1_W), QW(Q_F1), QS(Q_F1), scale_f16, NULL, FF, h);
 #pragma omp parallel for schedule(static)
-    for (size_t i = 0; i < (size_t)T * FF; i++) h[i] = gelu_tanh(h[i]);
-    dump(stages, ST_FF_H, h, (size_t)T * FF);
-    linear(h, T, FF, BW(W_FF2_W), QW(Q_F2), QS(Q_F2), scale_f16, NULL, D, a);
+    for (size_t i = 0; i < (size_t)nr * FF; i++) h[i] = gelu_tanh(h[i]);
+    dump(stages, ST_FF_H, h, (size_t)nr * FF);
+    linear(h, nr, FF, BW(W_FF2_W), QW(Q_F2), QS(Q_F2), scale_f16, NULL, D, a);
     free(h);
-    dump(stages, ST_S7_FF_OUT, a, TD);
+    dump(stages, ST_S7_FF_OUT, a, RD);
 #pragma omp parallel for schedule(static)
-    for (int t = 0; t < T; t++)
+    for (int t = 0; t < nr; t++)
         for (int c = 0; c < D; c++)
-            out[(size_t)t * D + c] = x_ca[(size_t)t * D + c] + a[(size_t)t * D + c] * ada(sst, tstab, tidx, t, 5, c);
+            out[(size_t)t * D + c] = x_ca[(size_t)t * D + c] + a[(size_t)t * D + c] * ada(sst, tstab, trow, t, 5, c);
     free(x);
     free(n);
     free(a);
     free(x_sa);
+    if (trow != trow_all) free(trow);
+    free(trow_all);
     return 1;
+}
+
+/* The whole block: every token (out [T][D]). */
+int orc_block_forward(const void* const* base, const int8_t* const* q8, const void* const* q8s, int scale_f16,
+                      const float* x_in, const float* tstab, int K, const int32_t* tidx, const float* ctx_in,
+                      int S, const float* pts2, const float* cs, const float* sn, int T, int chunk,
+                      int cross_chunk, real* out, real* const* stages) {
+    return block_rows(base, q8, q8s, scale_f16, x_in, tstab, K, tidx, ctx_in, S, pts2, cs, sn, T, chunk, cross_chunk,
+                      NULL, 0, out, stages);
+}
+
+/* Output rows rows[0 .. nr) of the block (out [nr][D]); each equals that row
+ * of orc_block_forward. */
+int orc_block_rows(const void* const* base, const int8_t* const* q8, const void* const* q8s, int scale_f16,
+                   const float* x_in, const float* tstab, int K, const int32_t* tidx, const float* ctx_in, int S,
+                   const float* pts2, const float* cs, const float* sn, int T, int chunk, int cross_chunk,
+                   const int* rows, int nr, real* out, real* const* stages) {
+    if (!rows) return 0;
+    return block_rows(base, q8, q8s, scale_f16, x_in, tstab, K, tidx, ctx_in, S, pts2, cs, sn, T, chunk, cross_chunk,
+                      rows, nr, out, stages);
 }
 
 /* Isolated linear for GEMM parity: y = x W^T (+ b), weight from bf16 or q8. */

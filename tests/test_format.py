@@ -131,6 +131,26 @@ def test_blob_error_paths(tmp_path):
         L.ltx_blob_close(h)
 
 
+def test_blob_manifest_bounds(tmp_path):
+    """Offsets and sizes that do not lie inside the blob (negative, or whose
+    sum would wrap past 2^64) and a non-positive alignment are refused when
+    the manifest is read."""
+    blob = (GOLD / "output" / "blob.bin").read_bytes()
+    man = json.loads((GOLD / "output" / "blob_manifest.json").read_text())
+    cases = [("neg_offset", lambda m: m["entries"][1].update(offset=-64), "TrailingBytes"),
+             ("neg_nbytes", lambda m: m["entries"][1].update(nbytes=-1), "TrailingBytes"),
+             ("wrap", lambda m: m["entries"][1].update(offset=64, nbytes=2 ** 63 - 1), "TrailingBytes"),
+             ("past_end", lambda m: m["entries"][-1].update(nbytes=m["entries"][-1]["nbytes"] + 1), "TrailingBytes"),
+             ("align0", lambda m: m.update(align=0), "Misaligned"),
+             ("align_neg", lambda m: m.update(align=-64), "Misaligned")]
+    for name, edit, err_name in cases:
+        m = json.loads(json.dumps(man))
+        edit(m)
+        _write_blob(tmp_path / name, blob, m)
+        ok, h, err = _open(tmp_path / name)
+        assert not ok and err_name in err, (name, err)
+
+
 def test_sha256_matches_hashlib():
     import hashlib
     for n in (0, 1, 55, 56, 63, 64, 65, 1000):

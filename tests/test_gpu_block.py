@@ -148,3 +148,38 @@ def test_zero_gates_give_identity(ctx, block0):
     w = ctx.upload(bt)
     got = run_block(ctx, w, inp, cos, sin, "f16")
     assert np.array_equal(got, inp["x"])
+
+
+def test_tidx_outside_rows_reads_row_zero(ctx, block0):
+    """An index outside 1 .. K-1 reads timestep row 0, as the reference's
+    select chain does (ltx/block.zig:47-67); no read leaves the table."""
+    T, S = 64, 32
+    say(f"tidx outside the table T={T} S={S} f16")
+    inp = synth.make_inputs(T, S, sigma=0.7)
+    assert inp["tstab"].shape[0] == 3
+    cos, sin = rt.rope_tables(inp["grid"])
+    bad, fixed = dict(inp), dict(inp)
+    bad["tidx"] = inp["tidx"].copy()
+    fixed["tidx"] = inp["tidx"].copy()
+    idx = [1, 5, 9, 30, 63]
+    bad["tidx"][idx] = [-1, 3, 100, -(2 ** 31), 2 ** 31 - 1]
+    fixed["tidx"][idx] = 0
+    w = ctx.upload(block0)
+    a = run_block(ctx, w, bad, cos, sin, "f16")
+    b = run_block(ctx, w, fixed, cos, sin, "f16")
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_blob_manifest_bounds_refused(ctx, block0):
+    """ltx_block_weights_from_blob refuses entries outside the blob (negative,
+    or a sum that would wrap) and misaligned offsets before reading a byte."""
+    say("blob upload with malformed manifests")
+    blob, man = bf.pack(block0)
+    import json
+    for edit, what in ((lambda e: e.update(offset=-64), "beyond the blob"),
+                       (lambda e: e.update(nbytes=2 ** 63 - 1), "beyond the blob"),
+                       (lambda e: e.update(offset=e["offset"] + 8), "Misaligned")):
+        m = json.loads(bf.manifest_json(man))
+        edit(m["entries"][3])
+        with pytest.raises(rt.LtxError, match=what):
+            ctx.upload_blob(blob, json.dumps(m), 0)

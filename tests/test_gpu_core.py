@@ -151,8 +151,8 @@ def denoise_case(core_np):
 
 @pytest.mark.parametrize("mode,gate", [("f16", 2e-3), ("f32", 1e-5)])
 def test_denoise_loop(ctx, core_dev, denoise_case, mode, gate):
-    """The GPU latent after each step against the oracle trajectory, and one
-    3-step call against three 1-step calls (bitwise)."""
+    """The GPU velocity and latent of each step against the oracle
+    trajectory, and one 3-step call against three 1-step calls (bitwise)."""
     c = denoise_case
     sig = c["sig"]
     say(f"denoise loop mode={mode} T=64 S=32 blocks=2 steps=3")
@@ -161,9 +161,13 @@ def test_denoise_loop(ctx, core_dev, denoise_case, mode, gate):
     md = rt.MODES[mode]
     for s in range(len(sig) - 1):
         ctx.denoise(ws, core_dev, dl, dc, dm, dt, dctx, dcos, dsin, sig[s:s + 2], mode=md)
+        vel = ctx.stage("velocity").view(torch.float32).reshape(64, 128).cpu().numpy()
+        rv = oracle.rel_rms(vel, c["want"][s][0])
         r = oracle.rel_rms(host(dl), c["want"][s][1])
-        print(f"step {s} sigma {sig[s]} -> {sig[s + 1]}: latent rel-RMS {r:.3e}", flush=True)
-        assert r <= gate, f"step {s}"
+        print(f"step {s} sigma {sig[s]} -> {sig[s + 1]}: velocity rel-RMS {rv:.3e}, latent rel-RMS {r:.3e}",
+              flush=True)
+        # both gated every step, as ltx/e2e_denoise.zig:314, 331 gate them
+        assert rv <= gate and r <= gate, f"step {s}"
     stepped = host(dl)
     dl2 = dev(c["lat0"])
     ctx.denoise(ws, core_dev, dl2, dc, dm, dt, dctx, dcos, dsin, sig, mode=md)

@@ -133,3 +133,50 @@ def test_full_size_zero_gates_identity(ctx, full):
     assert np.isfinite(got).all() and np.array_equal(got, inp1["x"])
     differ = got.view(np.uint32) != inp1["x"].view(np.uint32)
     assert (inp1["x"][differ] == 0).all()  # only the sign of zeros may change
+
+
+# ---- whole-block rows against the oracle at the full size -------------------
+
+# 256 output rows spread over the sequence, with the first and last tokens and
+# both sides of each change of the striped timestep row (T/7, 2T/7)
+ROWS = np.unique(np.concatenate([np.linspace(0, T - 1, 248).astype(np.int64),
+                                 [1, T // 7 - 1, T // 7, 2 * T // 7 - 1, 2 * T // 7, T - 2]]))
+_ROW_ORACLE = {}
+
+
+def _oracle_rows(key, bt, inp, cos, sin):
+    """The oracle's block rows: the modulated norm, K and V of all 28,672
+    tokens (the self-attention's keys), everything else for ROWS only;
+    blockwise attention in chunks of 1,024 as the reference runs it."""
+    if key not in _ROW_ORACLE:
+        say(f"  oracle rows ({len(ROWS)} of {T}, f64, {key} scales)")
+        _ROW_ORACLE[key] = oracle.block_forward(bt, inp, cos, sin, chunk=1024, stages=True, rows=ROWS)
+    return _ROW_ORACLE[key]
+
+
+@pytest.mark.parametrize("mode,scales", [("f16", "f16"), ("f16", "f32"), ("bf16", "f16")])
+def test_full_size_block_rows(ctx, request, mode, scales):
+    """The block at T = 28,672, S = 256, every projection int8: output rows,
+    and the self-attention, cross-attention and FFN residual branches of
+    those rows, against the f64 oracle (gate 2e-3 with fp16 operands; bf16
+    operands printed and held to 1.5e-2)."""
+    bt, inp, cos, sin = request.getfixturevalue("full" if scales == "f16" else "full_s32")
+    say(f"full-size block rows T={T} S={S} {mode} operands, {scales} scales")
+    w = ctx.upload(bt)
+    y = _run(ctx, w, inp, cos, sin, rt.MODES[mode])
+    assert torch.isfinite(y).all().item()
+    sel = torch.from_numpy(ROWS).cuda()
+    got = y[sel].cpu().numpy().astype(np.float64)
+    x_sa = _stage(ctx, "x_sa", torch.float32, (T, 4096), ROWS)
+    x_ca = _stage(ctx, "x_ca", torch.float32, (T, 4096), ROWS)
+    w.free()
+    del y
+    want, wst = _oracle_rows(scales, bt, inp, cos, sin)
+    x = inp["x"][ROWS].astype(np.float64)
+    r = {"y": oracle.rel_rms(got, want),
+         "sa_branch": oracle.rel_rms(x_sa - x, wst["s4_after_sa"] - x),
+         "ca_branch": oracle.rel_rms(x_ca - x_sa, wst["s5_ca_out"]),
+         "ff_branch": oracle.rel_rms(got - x_ca, want - wst["x_ca"])}
+    say("  " + " ".join(f"{k}={v:.2e}" for k, v in r.items()))
+    gate = 2e-3 if mode == "f16" else 1.5e-2
+    assert all(v <= gate for v in r.values()), r

@@ -299,3 +299,82 @@ def test_attention_variants(monkeypatch, variant):
         assert oracle.rel_rms(f64(out), want) <= 2e-3
     finally:
         c.close()
+
+
+# ---- the microbenchmark shapes (isolated GEMM and attention configurations) ----
+
+@pytest.mark.parametrize("mode", ["f16", "bf16"])
+def test_linear_q8_square_4096(ctx, mode):
+    """The 4096 x 4096 x 4096 W8A16 GEMM of the sweep: A N(0, 1) 16-bit,
+    W Student-t(3) x 0.02 int8 grouped-128 with fp16 scales, 16-bit output;
+    96 output rows against f64 with the exact weights (rel-RMS f16 <= 1e-3,
+    bf16 <= 6e-3: one rounding of the operands and of the output)."""
+    M = N = K = 4096
+    say(f"linear_q8 {M}x{K}x{N} mode={mode}")
+    m, dt = MODES[mode]
+    a, q, s, _ = _gemm_case(M, N, K, seed=44, scale_f16=True)
+    da = to16(a, dt).cuda()
+    y = torch.empty((M, N), dtype=dt, device="cuda")
+    ctx.linear_q8(da, torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(), None, y, mode=m)
+    torch.cuda.synchronize()
+    rows = np.linspace(0, M - 1, 96).astype(np.int64)
+    sel = torch.from_numpy(rows).cuda()
+    want = f64(da[sel]) @ oracle.dequant(q, s).astype(np.float64).T
+    r = oracle.rel_rms(f64(y[sel]), want)
+    say(f"  rel-RMS {r:.3e}")
+    assert r <= (1e-3 if mode == "f16" else 6e-3)
+
+
+@pytest.mark.parametrize("mode", ["f16", "bf16"])
+@pytest.mark.parametrize("L", [4096, 16384])
+def test_attention_long(ctx, mode, L):
+    """Self-attention at L = 4,096 and 16,384 (the sweep's tile-size lengths),
+    Q/K/V N(0, 1) 16-bit, no gate: 48 query rows of every head against f64
+    softmax attention over all L keys from the same 16-bit operands."""
+    say(f"attention L={L} mode={mode}")
+    m, dt = MODES[mode]
+    g = torch.Generator(device="cuda").manual_seed(L)
+    q = torch.randn((H_, L, 128), generator=g, device="cuda").to(dt)
+    k = torch.randn((H_, L, 128), generator=g, device="cuda").to(dt)
+    vt = torch.randn((H_, 128, L), generator=g, device="cuda").to(dt)
+    out = torch.empty((L, 4096), dtype=dt, device="cuda")
+    ctx.attention(q, k, vt, None, out, L, L, mode=m)
+    torch.cuda.synchronize()
+    rows = np.linspace(0, L - 1, 48).astype(np.int64)
+    sel = torch.from_numpy(rows).cuda()
+    q64, k64, v64 = f64(q[:, sel]), f64(k), f64(vt)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(128.0)))
+    want = np.empty((len(rows), 4096))
+    for h in range(H_):
+        sc = (q64[h] @ k64[h].T) * scale
+        p = np.exp(sc - sc.max(1, keepdims=True))
+        want[:, 128 * h:128 * h + 128] = (p @ v64[h].T) / p.sum(1, keepdims=True)
+    r = oracle.rel_rms(f64(out[sel]), want)
+    say(f"  rel-RMS {r:.3e}")
+    assert r <= (2e-3 if mode == "f16" else 1e-2)
+
+
+H_ = 32
+
+
+def test_linear_q8_onehot_large_f32_scales_f16(ctx):
+    """fp16 operands with f32 scales up to 2^99 (s 2^24 still finite): every
+    nonzero q * s is beyond the f16 range, so the operands are +-inf, and a
+    zero q gives 0, not NaN."""
+    say("linear_q8 one-hot f16 f32 scales 1e20..1e29.8")
+    got, want = _onehot_case(ctx, 1024, 512, 1024, seed=23, mode="f16", sf32=True, exp_range=(20, 29.8))
+    assert np.isinf(want).sum() > 1000 and (want == 0).sum() > 0
+    assert np.array_equal(got, want)
+
+
+def test_upload_refuses_f32_scales_out_of_range(ctx, block0):
+    """An f32 scale that is not finite or has magnitude >= 2^100 is refused at
+    upload (error ScaleRange)."""
+    say("upload with an out-of-range f32 scale")
+    for bad in (np.float32(2.0 ** 100), np.float32(np.inf), np.float32(np.nan), np.float32(-(2.0 ** 101))):
+        q8s = dict(block0.q8s)
+        s = q8s["k1"].copy()
+        s[7, 3] = bad
+        q8s["k1"] = s
+        with pytest.raises(rt.LtxError, match="ScaleRange"):
+            ctx.upload(bf.BlockTensors(0, block0.base, block0.q8, q8s))

@@ -207,3 +207,108 @@ def test_block_chunk_must_divide_keys(block0):
     blk = oracle.block_forward(block0, inp, c, s, chunk=10, cross_chunk=4)
     assert np.isfinite(dense).all()
     assert oracle.rel_rms(blk, dense) < 1e-12
+
+
+def test_block_rows_equal_whole_block(block0):
+    """The row-subset oracle (every token's keys and values, the other ops on
+    the chosen rows) returns exactly those rows of the whole block, stages
+    included."""
+    inp = synth.make_inputs(48, 8, sigma=0.7)
+    c, s = oracle.rope_tables(inp["grid"])
+    c, s = np.ascontiguousarray(c.transpose(1, 0, 2)), np.ascontiguousarray(s.transpose(1, 0, 2))
+    full, fst = oracle.block_forward(block0, inp, c, s, chunk=16, stages=True)
+    rows = np.array([0, 5, 6, 7, 30, 47])
+    part, pst = oracle.block_forward(block0, inp, c, s, chunk=16, stages=True, rows=rows)
+    assert np.array_equal(part, full[rows])
+    for name in oracle.ST_NAMES:
+        want = fst[name] if pst[name].shape[0] != len(rows) else fst[name][rows]
+        assert np.array_equal(pst[name], want), name
+    with pytest.raises(ValueError):
+        oracle.block_forward(block0, inp, c, s, chunk=16, rows=[48])
+
+
+def test_block_tidx_outside_rows_takes_row_zero(block0):
+    """adaVal's select chain (ltx/block.zig:47-67) starts from row 0 and
+    replaces it only for an index k in 1 .. K-1, so an index outside that
+    range reads row 0."""
+    inp = synth.make_inputs(16, 8, sigma=0.7)
+    assert inp["tstab"].shape[0] == 3
+    c, s = oracle.rope_tables(inp["grid"])
+    c, s = np.ascontiguousarray(c.transpose(1, 0, 2)), np.ascontiguousarray(s.transpose(1, 0, 2))
+    bad = dict(inp)
+    bad["tidx"] = inp["tidx"].copy()
+    bad["tidx"][[1, 5, 9, 12]] = [-1, 3, 100, -7]
+    fixed = dict(inp)
+    fixed["tidx"] = inp["tidx"].copy()
+    fixed["tidx"][[1, 5, 9, 12]] = 0
+    a = oracle.block_forward(block0, bad, c, s, chunk=16)
+    b = oracle.block_forward(block0, fixed, c, s, chunk=16)
+    assert np.array_equal(a, b)
+    assert not np.array_equal(a, oracle.block_forward(block0, inp, c, s, chunk=16))
+
+
+# ---- closed forms that pin the block's composition (tests/blockcases.py) ---
+
+@pytest.fixture(scope="module")
+def special(block0):
+    import blockcases
+
+    bt, inp = blockcases.special_case(block0, 16, 8)
+    c, s = oracle.rope_tables(inp["grid"])
+    c, s = np.ascontiguousarray(c.transpose(1, 0, 2)), np.ascontiguousarray(s.transpose(1, 0, 2))
+    out, st = oracle.block_forward(bt, inp, c, s, chunk=16, stages=True)
+    return bt, inp, c, s, out, st
+
+
+def test_oracle_self_attention_closed_form(special):
+    """Scale row ada1 = -1: every token's modulated norm is the shift row
+    ada0, every value row is v(ada0), so the gated self-attention output of
+    every token is 2 sigmoid(g(ada0)) v(ada0) whatever RoPE and the softmax
+    do (pins which AdaLN row is the shift and the 2 sigmoid gate taken from
+    the attention input, ltx/block.zig:237-241, 248-252)."""
+    import blockcases
+
+    bt, inp, _, _, _, st = special
+    merged, sa = blockcases.self_branch(bt, inp)
+    T = inp["x"].shape[0]
+    assert oracle.rel_rms(st["attn1_merged"], np.tile(merged, (T, 1))) < 1e-12
+    assert oracle.rel_rms(st["s4_after_sa"] - inp["x"].astype(np.float64), np.tile(sa, (T, 1))) < 1e-12
+
+
+def test_oracle_cross_attention_closed_form(special):
+    """Identical context rows: every key and value row is the same, so the
+    cross output of every query is v2(ctx (1 + kv[1]) + kv[0]) with
+    kv = psst + pts2 (pins the K/V modulation, ltx/block.zig:553-556, 291-306)."""
+    import blockcases
+
+    bt, inp, _, _, _, st = special
+    merged, ca = blockcases.cross_branch(bt, inp, st["attn_in"])
+    assert oracle.rel_rms(st["attn2_merged"], merged) < 1e-12
+    assert oracle.rel_rms(st["s5_ca_out"], ca) < 1e-12
+
+
+def test_oracle_ffn_closed_form(special):
+    """Scale row ada4 = -1: the FFN input is the shift row ada3 for every
+    token, so every FFN row is ff2(gelu(ff1(ada3))) times the gate row ada5
+    (ltx/block.zig:320-338, 569-573)."""
+    import blockcases
+
+    bt, inp, _, _, out, st = special
+    T = inp["x"].shape[0]
+    assert oracle.rel_rms(out - st["x_ca"], np.tile(blockcases.ffn_branch(bt, inp), (T, 1))) < 1e-12
+
+
+@pytest.mark.parametrize("mistake", ["ada_swap", "ca_swap", "ff_swap", "kv_swap", "kv_scale", "gate_no_2x"])
+def test_closed_form_catches_planted_mistakes(special, mistake):
+    """The oracle equals the closed form of the whole special-case block; the
+    numpy restatement with each planted mistake misses it by far more than
+    the f16 gate. (A RoPE sign error cannot show here, every value row being
+    the same, and LayerNorm for RMSNorm only weakly, through the cross
+    queries: the dense restatement and the RoPE table pins catch those.)"""
+    import blockcases
+
+    bt, inp, c, s, out, _ = special
+    want = blockcases.block_output(bt, inp)
+    assert oracle.rel_rms(out, want) < 1e-12
+    assert oracle.rel_rms(oracle.block_np(bt, inp, c, s), want) < 1e-12
+    assert oracle.rel_rms(oracle.block_np(bt, inp, c, s, mistake=mistake), want) > 4e-3
