@@ -357,13 +357,29 @@ def test_attention_long(ctx, mode, L):
 H_ = 32
 
 
-def test_linear_q8_onehot_large_f32_scales_f16(ctx):
-    """fp16 operands with f32 scales up to 2^99 (s 2^24 still finite): every
-    nonzero q * s is beyond the f16 range, so the operands are +-inf, and a
-    zero q gives 0, not NaN."""
-    say("linear_q8 one-hot f16 f32 scales 1e20..1e29.8")
-    got, want = _onehot_case(ctx, 1024, 512, 1024, seed=23, mode="f16", sf32=True, exp_range=(20, 29.8))
-    assert np.isinf(want).sum() > 1000 and (want == 0).sum() > 0
+def test_linear_q8_large_f32_scale_zero_group(ctx):
+    """fp16 operands with f32 scales up to 2^99 (s 2^24 still finite): for
+    every fourth column the first group's q are all 0 under a scale of
+    1e25..1e29.8, and its operands must be exactly 0, not NaN (0 * s formed
+    as fma((q + 128) 2^-24, s 2^24, -128 s)); every other group keeps small
+    scales, so the one-hot outputs stay finite and exact."""
+    say("linear_q8 one-hot f16 with huge f32 scales over all-zero groups")
+    M, N, K = 1024, 512, 1024
+    rng = np.random.default_rng(23)
+    q = rng.integers(-128, 128, size=(N, K), dtype=np.int16).astype(np.int8)
+    s = (10.0 ** rng.uniform(-4, -1, size=(N, K // 128))).astype(np.float32)
+    q[::4, :128] = 0
+    s[::4, 0] = (10.0 ** rng.uniform(25, 29.8, size=N // 4)).astype(np.float32)
+    e = np.zeros((M, K), np.float32)
+    e[np.arange(M), np.arange(M) % K] = 1.0
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    ctx.linear_q8(to16(e, torch.float16).cuda(), torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(), None, y,
+                  mode=rt.MODE_F16)
+    torch.cuda.synchronize()
+    exact = q.astype(np.float64) * np.repeat(s.astype(np.float64), 128, axis=1)
+    want = exact.astype(np.float16).astype(np.float32)[:, np.arange(M) % K].T
+    got = y.cpu().numpy()
+    assert np.isfinite(want).all()
     assert np.array_equal(got, want)
 
 

@@ -151,20 +151,30 @@ def test_block_closed_form(ctx, block0, mode):
     assert not bad, bad
 
 
-def test_int8_recipe_error_budgets(ctx, block0):
-    """The int8 block on the GPU (fp16 operands) against the f64 oracle of
-    the same block with its bf16 weights unquantised, with the budgets the
-    reference pre-registers for its own int8 probes
-    (ltx/block_conformance.zig:466-494): attention logits 5e-2, attention
-    output 2e-2, FFN output 5e-2, block output 2e-2. Student-t(3) weights;
-    the logits are those of the first 8 heads over all keys."""
+@pytest.mark.parametrize("dist", ["normal", "t3"])
+def test_int8_recipe_error_budgets(ctx, dist):
+    """The int8 block on the GPU (fp16 operands, the reference's int8 recipe:
+    q/k/v and FFN int8, f32 scales) against the f64 oracle of the same block
+    with its bf16 weights unquantised, with the budgets the reference
+    pre-registers for its own int8 probes (ltx/block_conformance.zig:466-494):
+    attention logits 5e-2, attention output (s3Attn1) 2e-2, FFN output
+    (s7FfOut) 5e-2, block output 2e-2. Logits: the first 8 heads, all keys.
+
+    Each probe is also measured for the oracle's own int8 block, which is the
+    recipe's error with no GPU arithmetic in it: the GPU may add at most 5 %
+    of it plus 1e-3. With N(0, 0.02) weights every budget holds. With
+    Student-t(3) x 0.02 weights the recipe itself puts the attention output
+    at 2.04e-2 (the group-128 absmax scale follows the outliers), just over
+    its 2e-2 budget, so that one probe is held to the recipe's own error."""
     T, S = 256, 64
-    say(f"int8 recipe error T={T} S={S} f16")
+    say(f"int8 recipe error T={T} S={S} f16 weights={dist}")
+    bt = synth.make_block(0, seed=1, dist=dist)
     inp = synth.make_inputs(T, S, sigma=0.7)
     cos, sin = rt.rope_tables(inp["grid"])
-    unq = bf.BlockTensors(block0.block, block0.base, {}, {})
+    unq = bf.BlockTensors(bt.block, bt.base, {}, {})
     want, wst = oracle.block_forward(unq, inp, cos, sin, chunk=16, stages=True)
-    w = ctx.upload(block0)
+    oq, oqst = oracle.block_forward(bt, inp, cos, sin, chunk=16, stages=True)
+    w = ctx.upload(bt)
     y = forward(ctx, w, inp, cos, sin, "f16")
     g = gpu_stages(ctx, "f16", T, S)
     w.free()
@@ -175,12 +185,20 @@ def test_int8_recipe_error_budgets(ctx, block0):
         k = k.reshape(T, H, HD)[:, :8].transpose(1, 0, 2)
         return q @ k.transpose(0, 2, 1)
 
-    r = {"logits": oracle.rel_rms(logits(g["q1"], g["k1"]), logits(wst["q1_roped"], wst["k1_roped"])),
-         "attention": oracle.rel_rms(g["x_sa"] - x, wst["s4_after_sa"] - x),
-         "ffn": oracle.rel_rms(y - g["x_ca"], want - wst["x_ca"]),
-         "block": oracle.rel_rms(y, want)}
+    def probes(q1, k1, x_sa, x_ca, yy):
+        # the attention output s3Attn1 = (x_sa - x) / ada2 and the FFN output
+        # s7FfOut = (y - x_ca) / ada5 are compared through their residual
+        # terms (x_sa - x and y - x_ca: the same vectors scaled per channel)
+        return {"logits": oracle.rel_rms(logits(q1, k1), logits(wst["q1_roped"], wst["k1_roped"])),
+                "attention": oracle.rel_rms(x_sa - x, wst["s4_after_sa"] - x),
+                "ffn": oracle.rel_rms(yy - x_ca, want - wst["x_ca"]),
+                "block": oracle.rel_rms(yy, want)}
+
+    r = probes(g["q1"], g["k1"], g["x_sa"], g["x_ca"], y)
+    rec = probes(oqst["q1_roped"], oqst["k1_roped"], oqst["s4_after_sa"], oqst["x_ca"], oq)
     budget = {"logits": 5e-2, "attention": 2e-2, "ffn": 5e-2, "block": 2e-2}
-    say("  " + " ".join(f"{k}={v:.2e} (budget {budget[k]:.0e})" for k, v in r.items()))
-    assert all(r[k] <= budget[k] for k in r), r
-    # and the int8 block is not the unquantised one: the probe measures something
-    assert r["ffn"] > 1e-3
+    say("  " + " ".join(f"{k}: gpu {r[k]:.2e} recipe {rec[k]:.2e} (budget {budget[k]:.0e})" for k in r))
+    assert all(r[k] <= 1.05 * rec[k] + 1e-3 for k in r), (r, rec)
+    held = [k for k in r if not (dist == "t3" and k == "attention")]
+    assert all(r[k] <= budget[k] for k in held), r
+    assert r["ffn"] > 1e-3  # the int8 block is not the unquantised one: the probe measures something
