@@ -168,6 +168,22 @@ int ltx_op_linear_q8(ltx_ctx* ctx, const void* a, const int8_t* q, const void* s
                      const float* bias, void* y, int out_f32, int M, int N, int K, int gelu, int mode,
                      void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): ltx_op_linear_q8 with the same arguments and results,
+ * calling no hipMalloc / hipFree. Its scratch (the weights as bytes q + 128,
+ * N * K bytes rounded up to 256, then the scale words, 4 N K / 128 bytes) is
+ * a static device array of LTX_NOALLOC_SCRATCH_BYTES on each GPU the library
+ * runs on, held until the process ends; a shape needing more is refused with
+ * an error. The kernels write all of the scratch they read on each call, so
+ * nothing carries over between calls, but every call on one GPU shares the
+ * array: calls that overlap on one GPU (other streams, contexts or threads)
+ * race. */
+#define LTX_NOALLOC_SCRATCH_BYTES (66u << 20)
+int ltx_op_linear_q8_noalloc(ltx_ctx* ctx, const void* a, const int8_t* q, const void* scales, int scale_f16,
+                             const float* bias, void* y, int out_f32, int M, int N, int K, int gelu, int mode,
+                             void* stream);
+
 /* Attention with per-(token, head) gate (gate logits glog [Lq][32] f32, or
  * NULL for no gate). F16/BF16: q, k [32][L][128] 16-bit, vt [32][128][Lkv]
  * 16-bit, out [Lq][4096] 16-bit. F32: q, k, v, out [L][4096] f32.

@@ -3,7 +3,8 @@
 1. Each kernel source csrc/k_*.hip -> a gfx950 code object (hipcc --genco).
 2. The code objects are embedded with .incbin into the host library, which
    loads them at ltx_init() with hipModuleLoadData.
-3. Host runtime (csrc/host/*.cpp, plain C++ over the HIP runtime API) + the
+3. Host runtime (csrc/host/*.cpp, plain C++ over the HIP runtime API; and
+   csrc/host/*.hip, host code with a device array of its own, by hipcc) + the
    embedded objects -> libltx_amd.so next to this file.
 
 Usage: python ltx-zml_amd/build.py [-v]
@@ -29,6 +30,11 @@ HOST = ["ltx_runtime", "ltx_forward", "ltx_weights", "ltx_rope", "ltx_loader", "
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "--genco",
     # packed-FP32 VALU forms are kept out of every kernel
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+HOST_HIP = ["ltx_noalloc"]
+HIP_HOST_FLAGS = [
+    "--offload-arch=gfx950", "-O2", "-std=c++17", "-fPIC", "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function", "-D__HIP_PLATFORM_AMD__",
@@ -61,6 +67,13 @@ def build(verbose: bool = False) -> pathlib.Path:
     for h in HOST:
         o = BUILD / f"{h}.o"
         jobs.append(["g++", *CXX_FLAGS, "-c", str(CSRC / "host" / f"{h}.cpp"), "-o", str(o)])
+        objs.append(o)
+    # host objects with device globals of their own (hipcc: registered with
+    # the HIP runtime when the library loads)
+    for h in HOST_HIP:
+        o = BUILD / f"{h}.o"
+        jobs.append([hipcc, *HIP_HOST_FLAGS, f"-I{CSRC}", f"-I{INCLUDE}", "-c", str(CSRC / "host" / f"{h}.hip"),
+                     "-o", str(o)])
         objs.append(o)
     with cf.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
         list(ex.map(lambda c: _run(c, verbose), jobs))

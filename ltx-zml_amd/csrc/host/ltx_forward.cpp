@@ -405,6 +405,63 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     set_stage(c, LTX_ST_V2, b.vt2, SD * 2);
 }
 
+bool linear_q8_needs_scratch(const ltx_ctx* c, int N, int K, int mode) {
+    (void)K;
+    return mode != LTX_MODE_F32 && c->gemm_q8 != 0 && N % 256 == 0;
+}
+
+// ltx_op_linear_q8 / _noalloc: in the 16-bit modes with the LDS-DMA kernel the
+// weights are first laid out as bytes q + 128 in sc.q and the scales as words
+// [K/128][N] in sc.pairs (both written whole before the GEMM reads them).
+void linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* scales, int scale_f16, const float* bias,
+               void* y, int out_f32, int M, int N, int K, int gelu, int mode, const LinearScratch& sc,
+               hipStream_t st) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 128) throw Error("bad GEMM shape (K must be a multiple of 128)");
+    if (mode != LTX_MODE_F16 && mode != LTX_MODE_BF16 && mode != LTX_MODE_F32) throw Error("unknown mode");
+    if (!a || !q || !scales || !y) throw Error("NULL tensor argument");
+    // Borrow the caller's buffers through a non-owning projection view.
+    LtxProj p;
+    p.N = N;
+    p.K = K;
+    p.q8 = true;
+    p.scale_f16 = scale_f16;
+    p.q.p = (void*)q;
+    p.s.p = (void*)scales;
+    p.bias.p = (void*)bias;
+    try {
+        if (mode == LTX_MODE_F32) {
+            if (!out_f32) throw Error("mode F32 writes f32 output");
+            LtxAda ada{};
+            gemm32(c, p, 0, N, (const float*)a, M, (float*)y, LTX_EPI_STORE, nullptr, ada, 0, gelu, st);
+        } else {
+            if (linear_q8_needs_scratch(c, N, K, mode)) {
+                if (!sc.q || !sc.pairs) throw Error("linear_q8: no scratch");
+                // the LDS-DMA kernel reads scale words [K/128][N]
+                const size_t n2 = (size_t)N * (K / LTX_GROUP);
+                LtxPairArgs pa{scales, sc.pairs, N, K / LTX_GROUP, scale_f16 ? 0 : 1};
+                c->launch("ltx_scale_pairs", (unsigned)((n2 + 255) / 256), 1, 1, 256, &pa, st);
+                p.s2.p = sc.pairs;
+                // and its weights as the bytes q + 128
+                const size_t nq = (size_t)N * K / 4;
+                LtxFlipArgs fa{(const uint32_t*)q, sc.q, nq};
+                c->launch("ltx_q8_flip", (unsigned)((nq + 255) / 256), 1, 1, 256, &fa, st);
+                p.q.p = sc.q;
+                p.qflip = true;
+            }
+            LtxGemmArgs g{};
+            g.out = y;
+            g.ldo = N;
+            g.gelu = gelu;
+            g.out_f32 = out_f32;
+            gemm16(c, mode, p, a, M, K, LTX_EPI_STORE, g, st);
+        }
+    } catch (...) {
+        p.q.p = p.s.p = p.s2.p = p.bias.p = nullptr;
+        throw;
+    }
+    p.q.p = p.s.p = p.s2.p = p.bias.p = nullptr;
+}
+
 }  // namespace ltx
 
 
@@ -423,51 +480,17 @@ int ltx_op_linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* sca
                      void* y, int out_f32, int M, int N, int K, int gelu, int mode, void* stream) {
     LTX_GUARD(c, {
         if (!c) throw ltx::Error("NULL context");
-        if (M <= 0 || N <= 0 || K <= 0 || K % 128) throw ltx::Error("bad GEMM shape (K must be a multiple of 128)");
         HIPC(hipSetDevice(c->device));
-        // Borrow the caller's buffers through a non-owning projection view.
-        LtxProj p;
-        p.N = N;
-        p.K = K;
-        p.q8 = true;
-        p.scale_f16 = scale_f16;
-        p.q.p = (void*)q;
-        p.s.p = (void*)scales;
-        p.bias.p = (void*)bias;
-        try {
-            if (mode == LTX_MODE_F32) {
-                if (!out_f32) throw ltx::Error("mode F32 writes f32 output");
-                LtxAda ada{};
-                ltx::gemm32(c, p, 0, N, (const float*)a, M, (float*)y, LTX_EPI_STORE, nullptr, ada, 0, gelu,
-                            (hipStream_t)stream);
-            } else {
-                if (c->gemm_q8 != 0 && N % 256 == 0) {
-                    // the LDS-DMA kernel reads scale words [K/128][N]
-                    const size_t n2 = (size_t)N * (K / LTX_GROUP);
-                    if (c->op_pairs.bytes < n2 * 4) c->op_pairs.alloc(n2 * 4);
-                    LtxPairArgs pa{scales, (uint32_t*)c->op_pairs.p, N, K / LTX_GROUP, scale_f16 ? 0 : 1};
-                    c->launch("ltx_scale_pairs", (unsigned)((n2 + 255) / 256), 1, 1, 256, &pa, (hipStream_t)stream);
-                    p.s2.p = c->op_pairs.p;
-                    // and its weights as the bytes q + 128
-                    const size_t nq = (size_t)N * K / 4;
-                    if (c->op_q.bytes < nq * 4) c->op_q.alloc(nq * 4);
-                    LtxFlipArgs fa{(const uint32_t*)q, (uint32_t*)c->op_q.p, nq};
-                    c->launch("ltx_q8_flip", (unsigned)((nq + 255) / 256), 1, 1, 256, &fa, (hipStream_t)stream);
-                    p.q.p = c->op_q.p;
-                    p.qflip = true;
-                }
-                LtxGemmArgs g{};
-                g.out = y;
-                g.ldo = N;
-                g.gelu = gelu;
-                g.out_f32 = out_f32;
-                ltx::gemm16(c, mode, p, a, M, K, LTX_EPI_STORE, g, (hipStream_t)stream);
-            }
-        } catch (...) {
-            p.q.p = p.s.p = p.s2.p = p.bias.p = nullptr;
-            throw;
+        ltx::LinearScratch sc{};
+        if (ltx::linear_q8_needs_scratch(c, N, K, mode)) {
+            // scratch owned by the context, grown as needed
+            const size_t nq = (size_t)N * K, np = (size_t)N * (K / LTX_GROUP) * 4;
+            if (c->op_q.bytes < nq) c->op_q.alloc(nq);
+            if (c->op_pairs.bytes < np) c->op_pairs.alloc(np);
+            sc.q = (uint32_t*)c->op_q.p;
+            sc.pairs = (uint32_t*)c->op_pairs.p;
         }
-        p.q.p = p.s.p = p.s2.p = p.bias.p = nullptr;
+        ltx::linear_q8(c, a, q, scales, scale_f16, bias, y, out_f32, M, N, K, gelu, mode, sc, (hipStream_t)stream);
     })
 }
 

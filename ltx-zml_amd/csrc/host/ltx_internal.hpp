@@ -114,6 +114,23 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
                    const float* sn, int T, float* y, int mode, hipStream_t st);
 uint16_t f32_to_f16_bits(float f);
 float bf16_bits_to_f32(uint16_t b);
+
+// Device scratch of the isolated int8 GEMM: the weights as bytes q + 128
+// (N * K bytes) and the scale words [K/128][N] (4 N K / 128 bytes).
+struct LinearScratch {
+    uint32_t* q;
+    uint32_t* pairs;
+};
+bool linear_q8_needs_scratch(const ltx_ctx* c, int N, int K, int mode);
+void linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* scales, int scale_f16, const float* bias,
+               void* y, int out_f32, int M, int N, int K, int gelu, int mode, const LinearScratch& sc,
+               hipStream_t st);
+
+// The static scratch array of ltx_op_linear_q8_noalloc (ltx_noalloc.hip):
+// noalloc_setup resolves its address on `device` (which must be current),
+// once per device; noalloc_scratch returns it (NULL before setup).
+void noalloc_setup(int device);
+void* noalloc_scratch(int device);
 }  // namespace ltx
 
 // Runs a body at the C boundary: exceptions become LTX_FAIL + error text.

@@ -139,6 +139,8 @@ int ltx_init(int device, ltx_ctx** out) {
         HIPC(hipGetDeviceProperties(&prop, device));
         if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
             throw ltx::Error(std::string("ltx_init: code objects are gfx950-only, device is ") + prop.gcnArchName);
+        // the static scratch of ltx_op_linear_q8_noalloc, resolved on this device
+        ltx::noalloc_setup(device);
         c = new ltx_ctx();
         c->device = device;
         c->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;

@@ -53,6 +53,7 @@ def lib() -> C.CDLL:
         "ltx_block_forward": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, vp, vp, vp, i32, vp, i32, vp]),
         "ltx_block_stage": (i32, [vp, i32, C.POINTER(vp), C.POINTER(u64)]),
         "ltx_op_linear_q8": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
+        "ltx_op_linear_q8_noalloc": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
         "ltx_op_attention": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
         "ltx_op_dequant": (i32, [vp, vp, vp, i32, i32, i32, vp, vp, i32, vp]),
         "ltx_rope_tables": (i32, [vp, i32, vp, vp, i32]),
@@ -245,14 +246,17 @@ class Context:
         return out
 
     # ---- operators ----
-    def linear_q8(self, a, q, s, bias, y, mode=MODE_F16, gelu=False, stream=None):
+    def linear_q8(self, a, q, s, bias, y, mode=MODE_F16, gelu=False, stream=None, noalloc=False):
+        """noalloc: the entry point with its scratch in the library's static
+        device array (ltx_op_linear_q8_noalloc)."""
         M, K = a.shape
         N = q.shape[0]
         import torch
         st = stream.cuda_stream if stream is not None else _current_stream()
-        self._check(lib().ltx_op_linear_q8(self.handle, _ptr(a), _ptr(q), _ptr(s), int(s.dtype == torch.float16),
-                                           _ptr(bias), _ptr(y), int(y.dtype == torch.float32), M, N, K, int(gelu),
-                                           mode, st), "ltx_op_linear_q8")
+        name = "ltx_op_linear_q8_noalloc" if noalloc else "ltx_op_linear_q8"
+        self._check(getattr(lib(), name)(self.handle, _ptr(a), _ptr(q), _ptr(s), int(s.dtype == torch.float16),
+                                         _ptr(bias), _ptr(y), int(y.dtype == torch.float32), M, N, K, int(gelu),
+                                         mode, st), name)
         return y
 
     def attention(self, q, k, v, glog, out, lq, lkv, mode=MODE_F16, stream=None, q_scaled=False):
