@@ -44,6 +44,49 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads() -> int:
+    """OpenMP threads of the CPU restatement: OMP_NUM_THREADS when set, else
+    the CPUs this process may run on."""
+    n = len(os.sched_getaffinity(0))
+    e = os.environ.get("OMP_NUM_THREADS")
+    return min(int(e), n) if e and e.isdigit() and int(e) > 0 else n
+
+
+def cpu_block_full(T: int, S: int) -> dict:
+    """The whole f32 CPU restatement of the block at T tokens, timed once
+    (one run: at T = 28,672 it takes minutes)."""
+    import oracle
+    from ltx_amd import runtime as rt
+    from ltx_amd import synth
+
+    threads = cpu_threads()
+    os.environ["OMP_NUM_THREADS"] = str(threads)
+    bt = synth.make_block(0, seed=1, dist="t3", classes=("qkv", "ff", "out"), scale_dtype="F16")
+    inp = synth.make_inputs(T, S, sigma=0.7)
+    cos, sin = rt.rope_tables(inp["grid"])
+    log(f"bench: whole f32 CPU block at T={T}, {threads} threads")
+    t0 = time.perf_counter()
+    y = oracle.block_forward(bt, inp, cos, sin, chunk=1024 if T % 1024 == 0 else 16, real="f32")
+    dt = time.perf_counter() - t0
+    f = flops(T, S)
+    assert y.shape == (T, D)
+    return {"metric": "whole f32 CPU restatement of the block, seconds", "value": round(dt, 2), "unit": "s",
+            "tokens": T, "text_tokens": S, "threads": threads, "affinity_cpus": len(os.sched_getaffinity(0)),
+            "cpu_model": cpu_model(), "tflops": round(sum(f.values()) / dt / 1e12, 4),
+            "kind": "port", "sample": "one run of the whole block (int8 weights, fp16 scales, blockwise attention "
+                                      "in chunks of 1024), after the inputs are built"}
+
+
 def cpu_baseline(T: int, S: int, threads: int, small=None) -> dict:
     """f32 oracle on the host: marginal GEMM rate (ff1 shape at two row counts,
     difference removes the per-call weight dequant), the dequant cost per
@@ -96,6 +139,7 @@ def cpu_baseline(T: int, S: int, threads: int, small=None) -> dict:
                                  "sigma 0.5): one warm-up, median of 5"}
     return {
         "value": round(total / est / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "affinity_cpus": len(os.sched_getaffinity(0)), "cpu_model": cpu_model(),
         "block_s_extrapolated": round(est, 2),
         "sample": (f"f32 CPU restatement of the reference graph (ZML CPU-PJRT unavailable offline), OpenMP "
                    f"{threads} threads: int8-dequant GEMM at the ff1 shape on {m1} and {m2} rows "
@@ -104,6 +148,66 @@ def cpu_baseline(T: int, S: int, threads: int, small=None) -> dict:
         "measured_s": round(t4 - t0, 2),
         **extra,
     }
+
+
+def denoise_steps(ctx, bt, T: int, S: int, nb: int, mode: int) -> dict:
+    """The stage-1 denoising loop (ltx/e2e_denoise.zig:218-336) over `nb`
+    resident copies of block `bt`: one ltx_denoise call per step, each timed
+    with HIP events on the launch stream, and after each step the
+    finite / RMS statistics of the velocity and the latent that the
+    reference's production pass prints (ltx/e2e_prod.zig:149-164)."""
+    import numpy as np
+    import torch
+
+    from ltx_amd import conditioning
+    from ltx_amd import runtime as rt
+    from ltx_amd import synth
+
+    t0 = time.time()
+    blocks = [ctx.upload(bt) for _ in range(nb)]
+    cw = ctx.upload_core(conditioning.make_core(7))
+    g = np.random.default_rng(3)
+    clean = g.standard_normal((T, 128)).astype(np.float32)
+    noise = g.standard_normal((T, 128)).astype(np.float32)
+    mask, tidx = conditioning.mask_rows(T)
+    ctx_tok = synth.rng(2, "ctx").standard_normal((S, D), dtype=np.float32)
+    cos, sin = rt.rope_tables(synth.grid_for_tokens(T))
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    dclean, dnoise, dmask, dtidx, dctx, dcos, dsin = (dev(a) for a in (clean, noise, mask, tidx, ctx_tok, cos, sin))
+    lat = torch.empty((T, 128), dtype=torch.float32, device="cuda")
+    sig = rt.sched_sigmas(1)
+    log(f"bench: denoise: {nb} blocks resident ({sum(b.nbytes for b in blocks) / 2 ** 30:.1f} GiB), "
+        f"inputs ready in {time.time() - t0:.1f}s")
+    stream = torch.cuda.current_stream()
+    # warm-up: one step
+    ctx.noise_init(dclean, dnoise, dmask, dtidx, float(sig[0]), lat)
+    ctx.denoise(blocks, cw, lat, dclean, dmask, dtidx, dctx, dcos, dsin, sig[:2], mode=mode)
+    torch.cuda.synchronize()
+    ctx.noise_init(dclean, dnoise, dmask, dtidx, float(sig[0]), lat)
+    ctx.range_count(reset=True)
+    steps = []
+    for s_ in range(len(sig) - 1):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        ctx.denoise(blocks, cw, lat, dclean, dmask, dtidx, dctx, dcos, dsin, sig[s_:s_ + 2], mode=mode,
+                    stream=stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        vel = ctx.stage("velocity").view(torch.float32)
+        steps.append({"sigma": float(sig[s_]), "sigma_next": float(sig[s_ + 1]), "ms": round(e0.elapsed_time(e1), 2),
+                      "velocity_finite": bool(torch.isfinite(vel).all().item()),
+                      "velocity_rms": round(float(vel.double().pow(2).mean().sqrt().item()), 5),
+                      "latent_finite": bool(torch.isfinite(lat).all().item()),
+                      "latent_rms": round(float(lat.double().pow(2).mean().sqrt().item()), 5)})
+        log(f"bench: denoise step {s_}: {steps[-1]['ms']:.1f} ms, latent rms {steps[-1]['latent_rms']}")
+    total = sum(x["ms"] for x in steps)
+    out = {"blocks": nb, "steps": len(steps), "denoise_s": round(total / 1e3, 3),
+           "ms_per_block_call": round(total / len(steps) / nb, 3),
+           "range_guard_out_of_range": ctx.range_count(reset=True), "per_step": steps}
+    for b in blocks:
+        b.free()
+    cw.free()
+    return out
 
 
 def denoise_bench(args) -> int:
@@ -272,6 +376,11 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true",
                     help="instead of the block line: time the isolated GEMM and attention kernels at the "
                          "microbenchmark shapes (f16 and bf16 operands) and print their own JSON line")
+    ap.add_argument("--no-denoise", action="store_true",
+                    help="leave the 48-block denoising loop out of the default line")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="instead of the block line: time the whole f32 CPU restatement of the block once at "
+                         "--tokens and print its own JSON line (minutes at 28,672 tokens; no GPU)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="run one plain device-to-device copy of this many MiB before the timed steps "
                          "(the known-size kernel that calibrates HBM byte counters)")
@@ -288,6 +397,9 @@ def main() -> int:
     from ltx_amd import synth
 
     T, S = args.tokens, args.text
+    if args.cpu_full:
+        print(json.dumps(cpu_block_full(T, S)), flush=True)
+        return 0
     if args.denoise:
         return denoise_bench(args)
     if args.sweep:
@@ -394,9 +506,15 @@ def main() -> int:
     res["t1024_block_ms"] = round(e0.elapsed_time(e1) / 20, 4)
     log(f"bench: T=1024 block {res['t1024_block_ms']:.3f} ms")
     w0.free()
+    if not args.no_denoise:
+        # the full-transformer loop: 48 resident int8 blocks x 8 stage-1 steps
+        # at the same 28,672 tokens (after the timed block region)
+        res["denoise"] = denoise_steps(ctx, bt, T, S, 48, mode)
+        log(f"bench: denoise {res['denoise']['denoise_s']:.2f} s, "
+            f"{res['denoise']['ms_per_block_call']:.2f} ms per block call")
     ctx.close()
     if not args.no_cpu_baseline:
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        threads = cpu_threads()
         log(f"bench: CPU baseline on {threads} threads")
         res["cpu_baseline"] = cpu_baseline(T, S, threads, small=(bt0, inp0, c0, s0))
     print(json.dumps(res), flush=True)

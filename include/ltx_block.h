@@ -152,6 +152,20 @@ enum {
 };
 int ltx_block_stage(ltx_ctx* ctx, int stage, void** dev_ptr, uint64_t* bytes);
 
+/* Range guard of the 16-bit modes. The reference computes in f32; here the
+ * MFMA operands (the modulated norms, Q, K, V, the attention outputs, the
+ * GELU hidden, the modulated context) are stored as f16 (LTX_MODE_F16) or
+ * bf16. Every block forward in those modes counts, on the device, the values
+ * it stored in 16 bits that were not finite or beyond the type's largest
+ * finite value (65504 for f16), in a counter of the context that accumulates
+ * over forwards (and ltx_denoise) until reset. This call waits for `stream`,
+ * returns the count and, when `reset`, sets it to 0 (the context starts at
+ * 0). A non-zero count means some activation left the 16-bit range: rerun in
+ * LTX_MODE_BF16 (the f32 exponent range) or LTX_MODE_F32. Weight operands
+ * are checked at upload instead: a forward in LTX_MODE_F16 refuses a block
+ * whose dequantised weights (128 |s|) or f16 copies exceed 65504. */
+int ltx_range_count(ltx_ctx* ctx, void* stream, uint64_t* count, int reset);
+
 /* ---- isolated operators (the microbenchmark surface, ltx/smoke.zig) ---- */
 
 /* y[M][N] = a[M][K] . dq4(q, s)^T (+ bias) with optional GELU-tanh.

@@ -33,6 +33,7 @@ __device__ __forceinline__ TileIdx tile_of(int bid, int tiles_m, int tiles_n) {
 template <typename T, int EPI, int NI, int NJ>
 __device__ __forceinline__ void gemm_epilogue(const LtxGemmArgs& a, const f32x16 (&acc)[NI][NJ], int rb, int cb,
                                               int n0) {
+    unsigned bad = 0;  // 16-bit stores out of range (range guard)
 #pragma unroll
     for (int i = 0; i < NI; i++) {
 #pragma unroll
@@ -51,10 +52,12 @@ __device__ __forceinline__ void gemm_epilogue(const LtxGemmArgs& a, const f32x16
                 float v = acc[i][j][r] + (a.bias ? a.bias[n] : 0.0f);
                 if (EPI == LTX_EPI_STORE) {
                     if (a.gelu) v = gelu_tanh(v);
-                    if (a.out_f32)
+                    if (a.out_f32) {
                         ((float*)a.out)[(size_t)m * a.ldo + n] = v;
-                    else
+                    } else {
                         ((uint16_t*)a.out)[(size_t)m * a.ldo + n] = Op<T>::bits(v);
+                        bad += out_of_range<T>(v);
+                    }
                 } else if (EPI == LTX_EPI_RESID_GATE) {
                     size_t o = (size_t)m * a.ldo + n;
                     ((float*)a.out)[o] = a.resid[o] + v * (gt[n] + gs[n]);
@@ -64,11 +67,13 @@ __device__ __forceinline__ void gemm_epilogue(const LtxGemmArgs& a, const f32x16
                     } else {
                         int c = n - a.nsplit;  // = h * 128 + d
                         ((uint16_t*)a.out2)[(size_t)c * a.M + m] = Op<T>::bits(v);
+                        bad += out_of_range<T>(v);
                     }
                 }
             }
         }
     }
+    range_report(a.sat, bad);
 }
 
 // LDS-staged epilogue: the same outputs as gemm_epilogue, for one wave's
@@ -86,6 +91,7 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
     const int lane = threadIdx.x & 63;
     const bool vt = EPI == LTX_EPI_QKV && n0 >= a.nsplit;
     const bool f32out = EPI != LTX_EPI_STORE || a.out_f32;
+    unsigned bad = 0;  // 16-bit stores out of range (range guard)
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         const int mb = mw + 32 * i;
@@ -129,6 +135,8 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
                 for (int e = 0; e < 8; e++) v[e] = patch[(8 * rg + e) * LD + cc] + bn;
                 const int m = mb + 8 * rg;
                 uint16_t* dst = (uint16_t*)a.out2 + (size_t)c * a.M + m;
+#pragma unroll
+                for (int e = 0; e < 8; e++) bad += m + e < a.M ? out_of_range<T>(v[e]) : 0u;
                 if ((a.M & 7) == 0 && m + 8 <= a.M) {
                     *(u32x4*)dst = u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
                                          pack2<T>(v[6], v[7])};
@@ -182,7 +190,10 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
                 *(u32x4*)((uint16_t*)a.out + (size_t)m * a.ldo + n) =
                     u32x4{pack2<T>(v0[0], v0[1]), pack2<T>(v0[2], v0[3]), pack2<T>(v1[0], v1[1]),
                           pack2<T>(v1[2], v1[3])};
+#pragma unroll
+                for (int e = 0; e < 4; e++) bad += out_of_range<T>(v0[e]) + out_of_range<T>(v1[e]);
             }
         }
     }
+    range_report(a.sat, bad);
 }

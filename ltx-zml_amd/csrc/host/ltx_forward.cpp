@@ -106,9 +106,14 @@ static LtxAda make_ada(const ltx_block_weights* w, const float* tstab, const int
     return a;
 }
 
+// The range guard's counter for the 16-bit modes (NULL in mode F32).
+static unsigned long long* sat_of(ltx_ctx* c, int mode) {
+    return mode == LTX_MODE_F32 ? nullptr : (unsigned long long*)c->range_ctr.p;
+}
+
 static void norm_mod(ltx_ctx* c, int mode, const float* x, void* y, LtxAda ada, int rows, int ish, int isc,
                      hipStream_t st) {
-    LtxNormArgs a{x, y, ada, rows, ish, isc};
+    LtxNormArgs a{x, y, ada, rows, ish, isc, sat_of(c, mode)};
     const char* k = mode == LTX_MODE_F32 ? "ltx_norm_mod_f32" : mode == LTX_MODE_BF16 ? "ltx_norm_mod_bf16" : "ltx_norm_mod_f16";
     c->launch(k, (rows + 3) / 4, 1, 1, 256, &a, st);  // four rows per workgroup (NORM_ROWS)
 }
@@ -173,14 +178,16 @@ static const float kAttnC = (float)(1.4426950408889634 / 11.313708498984761);
 // kAttnC for Q, so the attention reads scores in exp2 units, 1 for K.
 static void qknorm16(ltx_ctx* c, int mode, const float* x, int ldx, const void* w, const float* cs, const float* sn,
                      void* y, int rows, float oscale, hipStream_t st) {
-    LtxQkNormArgs a{x, (const float*)w, cs, sn, y, rows, ldx, oscale};
+    LtxQkNormArgs a{x, (const float*)w, cs, sn, y, rows, ldx, oscale, sat_of(c, mode)};
     c->launch(mode == LTX_MODE_BF16 ? "ltx_qknorm_bf16" : "ltx_qknorm_f16", rows, 1, 1, 256, &a, st);
 }
 
 // q_scaled: Q already carries kAttnC (the block path); else plain Q.
 static void attn16(ltx_ctx* c, int mode, const void* q, const void* k, const void* vt, const float* glog, void* out,
-                   int lq, int lkv, bool q_scaled, hipStream_t st, const char* label = nullptr) {
-    LtxAttnArgs a;
+                   int lq, int lkv, bool q_scaled, hipStream_t st, const char* label = nullptr,
+                   unsigned long long* sat = nullptr) {
+    LtxAttnArgs a{};
+    a.sat = sat;
     a.q = q;
     a.k = k;
     a.vt = vt;
@@ -324,6 +331,10 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     }
 
     if (!w->qkv1.q8 || !w->kv2.q8) throw Error("16-bit modes need int8 q/k/v weights (the QBlock recipe)");
+    if (mode == LTX_MODE_F16 && !(w->f16_max <= 65504.0f))
+        throw Error("mode F16: weight operands beyond the f16 range (largest |q s| or |w| " +
+                    std::to_string(w->f16_max) + " > 65504); run LTX_MODE_BF16");
+    unsigned long long* sat = sat_of(c, mode);
     Ws16 b;
     carve16(cv, b, T, S);
     // self-attention: n = modulate(rms(x), ada1, ada0); fused q|k|v GEMM
@@ -332,14 +343,15 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.out = b.qk32;
     g.out2 = b.vt1;
     g.nsplit = 2 * LTX_D;
+    g.sat = sat;
     gemm16(c, mode, w->qkv1, b.n_msa, T, LTX_D, LTX_EPI_QKV, g, st, "gemm:qkv1");
     gate16(c, mode, w->g1, b.n_msa, T, (float*)b.glog1, st);
     {  // q and k norms + RoPE in one pass (the RoPE rows read once)
         LtxQkNorm2Args qa{(const float*)b.qk32, (const float*)w->qn1.p, (const float*)w->kn1.p, cs, sn, b.qh1, b.kh1,
-                          T, 2 * LTX_D, kAttnC, 1.0f};
+                          T, 2 * LTX_D, kAttnC, 1.0f, sat};
         c->launch(mode == LTX_MODE_BF16 ? "ltx_qknorm2_bf16" : "ltx_qknorm2_f16", T, 1, 1, 256, &qa, st);
     }
-    attn16(c, mode, b.qh1, b.kh1, b.vt1, (const float*)b.glog1, b.o1, T, T, true, st, "attn:self");
+    attn16(c, mode, b.qh1, b.kh1, b.vt1, (const float*)b.glog1, b.o1, T, T, true, st, "attn:self", sat);
     g = LtxGemmArgs{};
     g.out = b.x_sa;
     g.resid = x;
@@ -355,16 +367,17 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.out_f32 = 1;
     gemm16(c, mode, w->q2, b.attn_in, T, LTX_D, LTX_EPI_STORE, g, st, "gemm:q2");
     gate16(c, mode, w->g2, b.attn_in, T, (float*)b.glog2, st);
-    LtxEncArgs ea{ctxv, (const float*)w->psst.p, pts2, b.enc, S};
+    LtxEncArgs ea{ctxv, (const float*)w->psst.p, pts2, b.enc, S, sat};
     c->launch(mode == LTX_MODE_BF16 ? "ltx_enc_bf16" : "ltx_enc_f16", S, 1, 1, 256, &ea, st);
     g = LtxGemmArgs{};
     g.out = b.k2_32;
     g.out2 = b.vt2;
     g.nsplit = LTX_D;
+    g.sat = sat;
     gemm16(c, mode, w->kv2, b.enc, S, LTX_D, LTX_EPI_QKV, g, st, "gemm:kv2");
     qknorm16(c, mode, (const float*)b.q2_32, LTX_D, w->qn2.p, nullptr, nullptr, b.qh2, T, kAttnC, st);
     qknorm16(c, mode, (const float*)b.k2_32, LTX_D, w->kn2.p, nullptr, nullptr, b.kh2, S, 1.0f, st);
-    attn16(c, mode, b.qh2, b.kh2, b.vt2, (const float*)b.glog2, b.o2, T, S, true, st, "attn:cross");
+    attn16(c, mode, b.qh2, b.kh2, b.vt2, (const float*)b.glog2, b.o2, T, S, true, st, "attn:cross", sat);
     g = LtxGemmArgs{};
     g.out = b.x_ca;
     g.resid = (const float*)b.x_sa;
@@ -378,6 +391,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.out = b.h;
     g.ldo = LTX_FF;
     g.gelu = 1;
+    g.sat = sat;
     gemm16(c, mode, w->f1, b.ff_in, T, LTX_D, LTX_EPI_STORE, g, st, "gemm:ff1");
     g = LtxGemmArgs{};
     g.out = y;

@@ -66,6 +66,7 @@ struct ltx_block_weights {
     LtxProj g1, g2;           // gate logits, N = 32 (16-bit only)
     ltx::DevBuf qn1, kn1, qn2, kn2;  // f32 [4096]
     ltx::DevBuf sst, psst;    // f32 [9][4096], [2][4096]
+    float f16_max = 0.0f;     // largest |weight operand| of mode F16 (above 65504: refused in F16)
     // f32-mode views of the fused projections' parts (bf16 originals / q8)
     uint64_t bytes = 0;
 };
@@ -87,6 +88,7 @@ struct ltx_ctx {
     std::string err;
     // workspace
     ltx::DevBuf ws;
+    ltx::DevBuf range_ctr;  // range guard: 16-bit stores out of range (u64), see ltx_range_count
     ltx::DevBuf op_pairs;  // scale pairs of the last ltx_op_linear_q8 call (f16 scales)
     ltx::DevBuf op_q;      // its weights as bytes q + 128
     ltx::DevBuf blob_stage;  // device copy of the blob image of the last streaming upload
@@ -114,6 +116,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
                    const float* sn, int T, float* y, int mode, hipStream_t st);
 uint16_t f32_to_f16_bits(float f);
 float bf16_bits_to_f32(uint16_t b);
+float f16_bits_to_f32(uint16_t h);
 
 // Device scratch of the isolated int8 GEMM: the weights as bytes q + 128
 // (N * K bytes) and the scale words [K/128][N] (4 N K / 128 bytes).

@@ -2,6 +2,7 @@
 #include <atomic>
 #include <cstdio>
 #include <cstdlib>
+#include <cmath>
 #include <cstring>
 
 #include "ltx_internal.hpp"
@@ -74,6 +75,15 @@ float bf16_bits_to_f32(uint16_t b) {
     return f;
 }
 
+// f16 bits -> f32 (exact): subnormals as m 2^-24, inf and NaN kept.
+float f16_bits_to_f32(uint16_t h) {
+    const uint32_t e = (h >> 10) & 0x1f, m = h & 0x3ff;
+    const float sign = (h & 0x8000u) ? -1.0f : 1.0f;
+    if (e == 0) return sign * std::ldexp((float)m, -24);
+    if (e == 31) return m ? NAN : sign * INFINITY;
+    return sign * std::ldexp((float)(m | 0x400u), (int)e - 25);
+}
+
 }  // namespace ltx
 
 hipFunction_t ltx_ctx::fn(const char* name) {
@@ -143,6 +153,9 @@ int ltx_init(int device, ltx_ctx** out) {
         ltx::noalloc_setup(device);
         c = new ltx_ctx();
         c->device = device;
+        // the range guard's counter, zero at creation
+        c->range_ctr.alloc(256);
+        HIPC(hipMemset(c->range_ctr.p, 0, 256));
         c->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
         // LTX_GEMM_GRID=tile: one workgroup per output tile instead of the
         // persistent grid of one per CU (A/B timing)
@@ -225,6 +238,21 @@ int ltx_profile_read(ltx_ctx* c, const char* substr, double* total_ms, int* coun
         }
         if (total_ms) *total_ms = tot;
         if (count) *count = n;
+    })
+}
+
+int ltx_range_count(ltx_ctx* c, void* stream, uint64_t* count, int reset) {
+    LTX_GUARD(c, {
+        if (!c || !count) throw ltx::Error("NULL argument");
+        HIPC(hipSetDevice(c->device));
+        HIPC(hipStreamSynchronize((hipStream_t)stream));
+        unsigned long long v = 0;
+        HIPC(hipMemcpy(&v, c->range_ctr.p, sizeof(v), hipMemcpyDeviceToHost));
+        *count = v;
+        if (reset) {
+            v = 0;
+            HIPC(hipMemcpy(c->range_ctr.p, &v, sizeof(v), hipMemcpyHostToDevice));
+        }
     })
 }
 

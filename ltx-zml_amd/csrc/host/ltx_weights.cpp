@@ -1,6 +1,7 @@
 // Weight upload: host pointers or a blob image + manifest -> the device form
 // the kernels consume (ltx/loader.zig:100-172: normalizeName, findEntry,
 // buildBlockBufs, buildQuantBufs).
+#include <cmath>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -176,6 +177,46 @@ static void check_f32_scales(const void* s, size_t n, const char* what) {
             throw Error(std::string("ScaleRange: f32 scale of ") + what + " is not finite or has magnitude >= 2^100");
 }
 
+// The largest magnitude among the 16-bit weight operands of mode F16: 128 max
+// |s| for each int8 projection (|q s| <= 128 |s|), max |w| for each bf16
+// weight converted to f16 (projections without int8 companions, gate logits).
+// Above 65504 those operands would round to inf.
+static float f16_operand_max(const void* const* base, const int8_t* const* q8, const void* const* q8s, int sf16) {
+    float m = 0.0f;
+    auto bf16_max = [&](int wi, size_t n) {
+        const uint16_t* w = (const uint16_t*)base[wi];
+        uint16_t mx = 0;
+        for (size_t i = 0; i < n; i++) mx = std::max<uint16_t>(mx, w[i] & 0x7fffu);
+        m = std::max(m, mx >= 0x7f80u ? INFINITY : bf16_bits_to_f32(mx));
+    };
+    for (int qi = 0; qi < LTX_Q_COUNT; qi++) {
+        int O, I;
+        q_dims(qi, O, I);
+        const size_t G = (size_t)O * (I / LTX_GROUP);
+        if (q8 && q8s && q8[qi] && q8s[qi]) {
+            float smax = 0.0f;
+            for (size_t g = 0; g < G; g++) {
+                float v;
+                if (sf16) {
+                    uint16_t h;
+                    std::memcpy(&h, (const char*)q8s[qi] + 2 * g, 2);
+                    v = f16_bits_to_f32(h);
+                } else {
+                    std::memcpy(&v, (const char*)q8s[qi] + 4 * g, 4);
+                }
+                v = std::fabs(v);
+                smax = std::isnan(v) ? INFINITY : std::max(smax, v);
+            }
+            m = std::max(m, 128.0f * smax);
+        } else {
+            bf16_max(kQBase[qi], (size_t)O * I);
+        }
+    }
+    bf16_max(LTX_W_G1_W, (size_t)LTX_H * LTX_D);
+    bf16_max(LTX_W_G2_W, (size_t)LTX_H * LTX_D);
+    return m;
+}
+
 static void check_scales(const void* const* q8s, const int8_t* const* q8, int sf16) {
     if (sf16 || !q8 || !q8s) return;
     for (int qi = 0; qi < LTX_Q_COUNT; qi++) {
@@ -191,8 +232,10 @@ ltx_block_weights* upload(ltx_ctx* c, const void* const* base, const int8_t* con
     for (int i = 0; i < LTX_W_COUNT; i++)
         if (!base[i]) throw Error(std::string("missing base weight ") + kBaseStems[i]);
     check_scales(q8s, q8, sf16);
+    const float f16max = f16_operand_max(base, q8, q8s, sf16);
     HIPC(hipSetDevice(c->device));
     auto* w = new ltx_block_weights();
+    w->f16_max = f16max;
     try {
         build_proj(w->qkv1, base, q8, q8s, sf16, {LTX_Q_Q1, LTX_Q_K1, LTX_Q_V1}, LTX_D, true);
         build_proj(w->o1, base, q8, q8s, sf16, {LTX_Q_O1}, LTX_D, true);
@@ -459,7 +502,22 @@ ltx_block_weights* upload_blob_async(ltx_ctx* c, const void* mem, uint64_t mem_b
     if (c->blob_stage.bytes < mem_bytes) c->blob_stage.alloc(mem_bytes);
     // the one DMA of the whole image (asynchronous when `mem` is pinned)
     HIPC(hipMemcpyAsync(c->blob_stage.p, mem, mem_bytes, hipMemcpyHostToDevice, st));
+    float f16max;
+    {  // the weight operands' range, read from the host image before the copy
+        const char* bytes = (const char*)mem;
+        const void* base[LTX_W_COUNT];
+        for (int i = 0; i < LTX_W_COUNT; i++) base[i] = bytes + L.base[i];
+        const int8_t* q8[LTX_Q_COUNT] = {};
+        const void* q8s[LTX_Q_COUNT] = {};
+        for (int qi = 0; qi < LTX_Q_COUNT; qi++)
+            if (L.q8[qi] >= 0) {
+                q8[qi] = (const int8_t*)(bytes + L.q8[qi]);
+                q8s[qi] = bytes + L.q8s[qi];
+            }
+        f16max = f16_operand_max(base, q8, q8s, L.sf16);
+    }
     ltx_block_weights* w = reuse ? reuse : new ltx_block_weights();
+    w->f16_max = f16max;
     try {
         DevCarve d{c, st, (const char*)c->blob_stage.p, reuse != nullptr};
         d.proj(w->qkv1, L, {LTX_Q_Q1, LTX_Q_K1, LTX_Q_V1}, LTX_D, true);

@@ -251,6 +251,7 @@ __device__ void attn_body(const LtxAttnArgs& a) {
 
     // out[q][h * 128 + d] = O^T[d][q] / l * 2 sigmoid(glog[q][h])
     uint16_t* out = (uint16_t*)a.out;
+    unsigned bad = 0;  // 16-bit outputs out of range (range guard)
 #pragma unroll
     for (int qb = 0; qb < QB; qb++) {
         const float lt = l[qb] + __shfl_xor(l[qb], 32, 64);
@@ -266,9 +267,12 @@ __device__ void attn_body(const LtxAttnArgs& a) {
                 u32x2 pk2 = {Op<T>::cvt2(o[qb][db][4 * rg] * sc, o[qb][db][4 * rg + 1] * sc),
                              Op<T>::cvt2(o[qb][db][4 * rg + 2] * sc, o[qb][db][4 * rg + 3] * sc)};
                 *(u32x2*)(out + (size_t)q * LTX_D + h * LTX_HD + d) = pk2;
+#pragma unroll
+                for (int e = 0; e < 4; e++) bad += out_of_range<T>(o[qb][db][4 * rg + e] * sc);
             }
         }
     }
+    range_report(a.sat, bad);
 }
 
 #define ATTN_KERNEL(NAME, T, QB, FULL, NW, PS)                                                      \
@@ -954,6 +958,7 @@ struct AttnPP {
         const float sc = gg / lt;
         uint16_t* patch = (uint16_t*)(w < 3 ? app_k0 + 4608 * w : w < 6 ? app_k1 + 4608 * (w - 3) : app_k2 + 4608 * (w - 6));
         uint16_t* out = (uint16_t*)a.out;
+        unsigned bad = 0;  // 16-bit outputs out of range (range guard)
 #pragma unroll
         for (int half = 0; half < 2; half++) {
 #pragma unroll
@@ -965,6 +970,8 @@ struct AttnPP {
                     *(u32x2*)(patch + r * 72 + d) =
                         u32x2{Op<T>::cvt2(o[db][4 * rg] * sc, o[db][4 * rg + 1] * sc),
                               Op<T>::cvt2(o[db][4 * rg + 2] * sc, o[db][4 * rg + 3] * sc)};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) bad += out_of_range<T>(o[db][4 * rg + e] * sc);
                 }
             }
 #pragma unroll
@@ -975,6 +982,7 @@ struct AttnPP {
                 if (q < lq) *(u32x4*)(out + (size_t)q * LTX_D + h * LTX_HD + 64 * half + 8 * c) = v;
             }
         }
+        range_report(a.sat, qr < lq ? bad : 0u);
     }
 };
 

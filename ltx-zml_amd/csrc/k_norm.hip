@@ -38,6 +38,7 @@ __device__ void norm_mod_body(const LtxNormArgs& a) {
         }
     };
     if (shared_mod) load_mod(ada_row(a.ada, row0));
+    unsigned bad = 0;  // 16-bit stores out of range (range guard)
     for (int k = 0; k < nr; k++) {
         const int row = row0 + k;
         const float4* x = (const float4*)(a.x + (size_t)row * LTX_D);
@@ -67,12 +68,17 @@ __device__ void norm_mod_body(const LtxNormArgs& a) {
             } else if (OUT == 0) {
                 u32x2 p = {pack2<_Float16>(o[0], o[1]), pack2<_Float16>(o[2], o[3])};
                 *(u32x2*)((uint16_t*)a.y + off) = p;
+#pragma unroll
+                for (int j = 0; j < 4; j++) bad += out_of_range<_Float16>(o[j]);
             } else {
                 u32x2 p = {pack2<__bf16>(o[0], o[1]), pack2<__bf16>(o[2], o[3])};
                 *(u32x2*)((uint16_t*)a.y + off) = p;
+#pragma unroll
+                for (int j = 0; j < 4; j++) bad += out_of_range<__bf16>(o[j]);
             }
         }
     }
+    range_report(a.sat, bad);
 }
 
 extern "C" __global__ void __launch_bounds__(256) ltx_norm_mod_f16(const LtxNormArgs a) { norm_mod_body<0>(a); }
@@ -84,6 +90,7 @@ template <int OUT>
 __device__ void enc_body(const LtxEncArgs& a) {
     int row = blockIdx.x;
     if (row >= a.rows) return;
+    unsigned bad = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         int c = 4 * (threadIdx.x + 256 * i);
@@ -98,11 +105,16 @@ __device__ void enc_body(const LtxEncArgs& a) {
         } else if (OUT == 0) {
             u32x2 p = {pack2<_Float16>(o[0], o[1]), pack2<_Float16>(o[2], o[3])};
             *(u32x2*)((uint16_t*)a.y + off) = p;
+#pragma unroll
+            for (int j = 0; j < 4; j++) bad += out_of_range<_Float16>(o[j]);
         } else {
             u32x2 p = {pack2<__bf16>(o[0], o[1]), pack2<__bf16>(o[2], o[3])};
             *(u32x2*)((uint16_t*)a.y + off) = p;
+#pragma unroll
+            for (int j = 0; j < 4; j++) bad += out_of_range<__bf16>(o[j]);
         }
     }
+    range_report(a.sat, bad);
 }
 
 extern "C" __global__ void __launch_bounds__(256) ltx_enc_f16(const LtxEncArgs a) { enc_body<0>(a); }
@@ -173,6 +185,10 @@ __device__ void qknorm_body(const LtxQkNormArgs& a) {
     u32x4 phi = {pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3]), pack2<T>(hi[4], hi[5]), pack2<T>(hi[6], hi[7])};
     *(u32x4*)(y + f0) = plo;
     *(u32x4*)(y + 64 + f0) = phi;
+    unsigned bad = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) bad += out_of_range<T>(lo[j]) + out_of_range<T>(hi[j]);
+    range_report(a.sat, bad);
 }
 
 // q and k of one token together (same thread layout as qknorm_body), the
@@ -240,6 +256,12 @@ __device__ void qknorm2_body(const LtxQkNorm2Args& a) {
         *(u32x4*)(y + 64 + f0) =
             u32x4{pack2<T>(u[0], u[1]), pack2<T>(u[2], u[3]), pack2<T>(u[4], u[5]), pack2<T>(u[6], u[7])};
     }
+    unsigned bad = 0;
+#pragma unroll
+    for (int p = 0; p < 2; p++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) bad += out_of_range<T>(lo[p][j]) + out_of_range<T>(hi[p][j]);
+    range_report(a.sat, bad);
 }
 
 extern "C" __global__ void __launch_bounds__(256) ltx_qknorm2_f16(const LtxQkNorm2Args a) { qknorm2_body<_Float16>(a); }

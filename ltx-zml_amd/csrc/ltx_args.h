@@ -9,6 +9,10 @@
 extern "C" {
 #endif
 
+// Range guard: kernels that store 16-bit activations add to *sat the number of
+// stored values that are not finite or exceed the type's largest finite value
+// (65504 for f16), when sat is not NULL.
+
 // Model geometry of the LTX-2.5 video block (ltx/block.zig:14-18).
 #define LTX_D 4096
 #define LTX_H 32
@@ -33,6 +37,7 @@ typedef struct {
     LtxAda ada;
     int rows;
     int ish, isc;    // ada row indices for shift and scale; isc < 0: plain rms
+    unsigned long long* sat;  // range guard counter (16-bit outputs) or NULL
 } LtxNormArgs;
 
 // Cross-attention K/V modulation (ltx/block.zig:553-556):
@@ -43,6 +48,7 @@ typedef struct {
     const float* pts2;  // [2][D]
     void* y;            // [S][D]
     int rows;
+    unsigned long long* sat;  // range guard counter (16-bit outputs) or NULL
 } LtxEncArgs;
 
 // Epilogue kinds of the W8A16 / W16A16 GEMM.
@@ -78,6 +84,7 @@ typedef struct {
     int tiles_m, tiles_n; // grid geometry (filled by host)
     uint32_t qxor;        // int8 kinds: XOR taking each weight byte to q + 128 (0x80808080 for plain int8,
                           // 0 for bytes stored as q + 128); the LDS-DMA kernels take the latter only
+    unsigned long long* sat;  // range guard counter of the 16-bit outputs (V^T, 16-bit stores) or NULL
 } LtxGemmArgs;
 
 // Full-row qk RMSNorm (weighted, over all 4096 channels) + optional split-half
@@ -91,6 +98,7 @@ typedef struct {
     int rows;
     int ldx;
     float oscale;       // applied before the 16-bit rounding (1, or the attention's exponent scale for Q)
+    unsigned long long* sat;  // range guard counter or NULL
 } LtxQkNormArgs;
 
 // The self-attention's q and k rows of one token in one pass (the RoPE rows
@@ -106,6 +114,7 @@ typedef struct {
     int rows;
     int ldx;
     float oscale_q, oscale_k;
+    unsigned long long* sat;  // range guard counter or NULL
 } LtxQkNorm2Args;
 
 // Blockwise online-softmax attention with per-(token, head) gate.
@@ -120,6 +129,7 @@ typedef struct {
     int lq, lkv;
     float scale_log2;   // softmax scale * log2(e)
     int q_tiles;        // ceil(lq / q-tile)
+    unsigned long long* sat;  // range guard counter of the 16-bit output or NULL
 } LtxAttnArgs;
 
 // Gate logits: glog[t][h] = a[t] . gw[h] + gb[h] (N = 32 heads).

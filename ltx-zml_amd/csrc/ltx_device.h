@@ -75,6 +75,27 @@ struct Op<__bf16> {
     }
 };
 
+// Range guard of the 16-bit stores: 1 when v is not finite or beyond the
+// operand type's largest finite value (its 16-bit rounding saturates to inf).
+template <typename T>
+struct RangeMax;
+template <>
+struct RangeMax<_Float16> {
+    static constexpr float v = 65504.0f;
+};
+template <>
+struct RangeMax<__bf16> {
+    static constexpr float v = 3.38953139e38f;
+};
+template <typename T>
+__device__ __forceinline__ unsigned out_of_range(float v) {
+    return __builtin_fabsf(v) <= RangeMax<T>::v ? 0u : 1u;
+}
+// One vector atomic per lane that saw any (none in the ordinary case).
+__device__ __forceinline__ void range_report(unsigned long long* sat, unsigned n) {
+    if (n && sat) atomicAdd(sat, (unsigned long long)n);
+}
+
 // Pack two f32 into two 16-bit lanes of one dword (lo = a).
 template <typename T>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {

@@ -52,6 +52,7 @@ def lib() -> C.CDLL:
         "ltx_block_weights_bytes": (u64, [vp]),
         "ltx_block_forward": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, vp, vp, vp, i32, vp, i32, vp]),
         "ltx_block_stage": (i32, [vp, i32, C.POINTER(vp), C.POINTER(u64)]),
+        "ltx_range_count": (i32, [vp, vp, C.POINTER(u64), i32]),
         "ltx_op_linear_q8": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
         "ltx_op_linear_q8_noalloc": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
         "ltx_op_attention": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
@@ -235,6 +236,13 @@ class Context:
                                             _ptr(pts2), _ptr(cos), _ptr(sin), T, _ptr(y), mode, st),
                     "ltx_block_forward")
         return y
+
+    def range_count(self, reset: bool = True, stream=None) -> int:
+        """16-bit stores out of range since the last reset (ltx_range_count)."""
+        st = stream.cuda_stream if stream is not None else _current_stream()
+        n = C.c_uint64()
+        self._check(lib().ltx_range_count(self.handle, st, C.byref(n), int(reset)), "ltx_range_count")
+        return n.value
 
     def stage(self, name: str):
         import torch
