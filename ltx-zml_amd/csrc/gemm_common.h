@@ -2,7 +2,7 @@
 #pragma once
 #include "ltx_device.h"
 
-#define GM 8  // M-tiles per rasterisation group
+#define GM 4  // M-tiles per rasterisation group
 
 struct TileIdx {
     int tm, tn;
@@ -63,7 +63,8 @@ __device__ __forceinline__ void gemm_epilogue(const LtxGemmArgs& a, const f32x16
                     ((float*)a.out)[o] = a.resid[o] + v * (gt[n] + gs[n]);
                 } else {  // QKV
                     if (n0 < a.nsplit) {
-                        ((float*)a.out)[(size_t)m * a.nsplit + n] = v;
+                        ((uint16_t*)a.out)[(size_t)m * a.nsplit + n] = Op<T>::bits(v);
+                        bad += out_of_range<T>(v);
                     } else {
                         int c = n - a.nsplit;  // = h * 128 + d
                         ((uint16_t*)a.out2)[(size_t)c * a.M + m] = Op<T>::bits(v);
@@ -90,7 +91,8 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
     constexpr int WN = 32 * NJ, LD = WN + 8;
     const int lane = threadIdx.x & 63;
     const bool vt = EPI == LTX_EPI_QKV && n0 >= a.nsplit;
-    const bool f32out = EPI != LTX_EPI_STORE || a.out_f32;
+    const bool f32out = EPI == LTX_EPI_RESID_GATE || (EPI == LTX_EPI_STORE && a.out_f32);
+    const int ldo = EPI == LTX_EPI_QKV ? a.nsplit : a.ldo;  // 16-bit rows: q | k [M][nsplit] or [M][ldo]
     unsigned bad = 0;  // 16-bit stores out of range (range guard)
 #pragma unroll
     for (int i = 0; i < NI; i++) {
@@ -161,11 +163,9 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
                 if (EPI == LTX_EPI_STORE) {
                     if (a.gelu) v = f32x4{gelu_tanh(v[0]), gelu_tanh(v[1]), gelu_tanh(v[2]), gelu_tanh(v[3])};
                     *(f32x4*)((float*)a.out + (size_t)m * a.ldo + n) = v;
-                } else if (EPI == LTX_EPI_RESID_GATE) {
+                } else {  // gated residual
                     const size_t o = (size_t)m * a.ldo + n;
                     *(f32x4*)((float*)a.out + o) = rs[p] + v * (gt[p] + gs);
-                } else {  // q | k part of the fused QKV projection
-                    *(f32x4*)((float*)a.out + (size_t)m * a.nsplit + n) = v;
                 }
             }
         } else {  // 16-bit rows: 8 columns a lane
@@ -183,11 +183,11 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
                 if (m >= a.M) continue;
                 f32x4 v0 = *(const f32x4*)(patch + rr * LD + c8) + b0;
                 f32x4 v1 = *(const f32x4*)(patch + rr * LD + c8 + 4) + b1;
-                if (a.gelu) {
+                if (EPI == LTX_EPI_STORE && a.gelu) {
                     v0 = f32x4{gelu_tanh(v0[0]), gelu_tanh(v0[1]), gelu_tanh(v0[2]), gelu_tanh(v0[3])};
                     v1 = f32x4{gelu_tanh(v1[0]), gelu_tanh(v1[1]), gelu_tanh(v1[2]), gelu_tanh(v1[3])};
                 }
-                *(u32x4*)((uint16_t*)a.out + (size_t)m * a.ldo + n) =
+                *(u32x4*)((uint16_t*)a.out + (size_t)m * ldo + n) =
                     u32x4{pack2<T>(v0[0], v0[1]), pack2<T>(v0[2], v0[3]), pack2<T>(v1[0], v1[1]),
                           pack2<T>(v1[2], v1[3])};
 #pragma unroll

@@ -27,14 +27,14 @@ struct Carve {
 };
 
 struct Ws16 {
-    void *n_msa, *qk32, *vt1, *qh1, *kh1, *glog1, *o1, *x_sa, *attn_in, *q2_32, *glog2, *enc, *k2_32, *vt2, *qh2,
+    void *n_msa, *qk16, *vt1, *qh1, *kh1, *glog1, *o1, *x_sa, *attn_in, *q2_16, *glog2, *enc, *k2_16, *vt2, *qh2,
         *kh2, *o2, *x_ca, *ff_in, *h;
 };
 
 static void carve16(Carve& c, Ws16& w, size_t T, size_t S) {
     const size_t D = LTX_D;
     w.n_msa = c.take(T * D * 2);
-    w.qk32 = c.take(T * 2 * D * 4);
+    w.qk16 = c.take(T * 2 * D * 2);
     w.vt1 = c.take(T * D * 2);
     w.qh1 = c.take(T * D * 2);
     w.kh1 = c.take(T * D * 2);
@@ -42,10 +42,10 @@ static void carve16(Carve& c, Ws16& w, size_t T, size_t S) {
     w.o1 = c.take(T * D * 2);
     w.x_sa = c.take(T * D * 4);
     w.attn_in = c.take(T * D * 2);
-    w.q2_32 = c.take(T * D * 4);
+    w.q2_16 = c.take(T * D * 2);
     w.glog2 = c.take(T * LTX_H * 4);
     w.enc = c.take(S * D * 2);
-    w.k2_32 = c.take(S * D * 4);
+    w.k2_16 = c.take(S * D * 2);
     w.vt2 = c.take(S * D * 2);
     w.qh2 = c.take(T * D * 2);
     w.kh2 = c.take(S * D * 2);
@@ -176,7 +176,7 @@ static const float kAttnC = (float)(1.4426950408889634 / 11.313708498984761);
 
 // oscale multiplies the normed (and roped) rows before the 16-bit rounding:
 // kAttnC for Q, so the attention reads scores in exp2 units, 1 for K.
-static void qknorm16(ltx_ctx* c, int mode, const float* x, int ldx, const void* w, const float* cs, const float* sn,
+static void qknorm16(ltx_ctx* c, int mode, const void* x, int ldx, const void* w, const float* cs, const float* sn,
                      void* y, int rows, float oscale, hipStream_t st) {
     LtxQkNormArgs a{x, (const float*)w, cs, sn, y, rows, ldx, oscale, sat_of(c, mode)};
     c->launch(mode == LTX_MODE_BF16 ? "ltx_qknorm_bf16" : "ltx_qknorm_f16", rows, 1, 1, 256, &a, st);
@@ -260,6 +260,13 @@ static void attn32(ltx_ctx* c, const float* q, const float* k, const float* v, c
     c->launch("ltx_attn_f32", (lq + 63) / 64, LTX_H, 1, 64, &a, st);
 }
 
+// `to` runs what it is given next only after everything enqueued so far on
+// `from` (event e).
+static void stream_after(hipStream_t to, hipStream_t from, hipEvent_t e) {
+    HIPC(hipEventRecord(e, from));
+    HIPC(hipStreamWaitEvent(to, e, 0));
+}
+
 static void set_stage(ltx_ctx* c, int id, void* p, size_t bytes) {
     c->stage_ptr[id] = p;
     c->stage_bytes[id] = bytes;
@@ -340,17 +347,25 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     // self-attention: n = modulate(rms(x), ada1, ada0); fused q|k|v GEMM
     norm_mod(c, mode, x, b.n_msa, ada, T, 0, 1, st);
     LtxGemmArgs g{};
-    g.out = b.qk32;
+    g.out = b.qk16;
     g.out2 = b.vt1;
     g.nsplit = 2 * LTX_D;
     g.sat = sat;
     gemm16(c, mode, w->qkv1, b.n_msa, T, LTX_D, LTX_EPI_QKV, g, st, "gemm:qkv1");
-    gate16(c, mode, w->g1, b.n_msa, T, (float*)b.glog1, st);
+    // The self-attention gate logits on the side stream, beside the q/k
+    // norms (both read only what the GEMMs above wrote). Side work starts
+    // after the persistent GEMM before it, whose one-workgroup-per-CU grid it
+    // would otherwise hold back, and ends before the attention, which it
+    // would slow as much as it gains.
+    hipStream_t sd = c->side;
+    stream_after(sd, st, c->side_ev[0]);
+    gate16(c, mode, w->g1, b.n_msa, T, (float*)b.glog1, sd);
     {  // q and k norms + RoPE in one pass (the RoPE rows read once)
-        LtxQkNorm2Args qa{(const float*)b.qk32, (const float*)w->qn1.p, (const float*)w->kn1.p, cs, sn, b.qh1, b.kh1,
+        LtxQkNorm2Args qa{b.qk16, (const float*)w->qn1.p, (const float*)w->kn1.p, cs, sn, b.qh1, b.kh1,
                           T, 2 * LTX_D, kAttnC, 1.0f, sat};
         c->launch(mode == LTX_MODE_BF16 ? "ltx_qknorm2_bf16" : "ltx_qknorm2_f16", T, 1, 1, 256, &qa, st);
     }
+    stream_after(st, sd, c->side_ev[1]);
     attn16(c, mode, b.qh1, b.kh1, b.vt1, (const float*)b.glog1, b.o1, T, T, true, st, "attn:self", sat);
     g = LtxGemmArgs{};
     g.out = b.x_sa;
@@ -362,21 +377,25 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     // cross-attention
     norm_mod(c, mode, (const float*)b.x_sa, b.attn_in, ada, T, 6, 7, st);
     g = LtxGemmArgs{};
-    g.out = b.q2_32;
+    g.out = b.q2_16;
     g.ldo = LTX_D;
-    g.out_f32 = 1;
+    g.sat = sat;
     gemm16(c, mode, w->q2, b.attn_in, T, LTX_D, LTX_EPI_STORE, g, st, "gemm:q2");
-    gate16(c, mode, w->g2, b.attn_in, T, (float*)b.glog2, st);
+    // the cross-attention gate logits on the side stream, beside the context
+    // side (K/V modulation, k|v GEMM) and the q and k norms
+    stream_after(sd, st, c->side_ev[2]);
+    gate16(c, mode, w->g2, b.attn_in, T, (float*)b.glog2, sd);
     LtxEncArgs ea{ctxv, (const float*)w->psst.p, pts2, b.enc, S, sat};
     c->launch(mode == LTX_MODE_BF16 ? "ltx_enc_bf16" : "ltx_enc_f16", S, 1, 1, 256, &ea, st);
     g = LtxGemmArgs{};
-    g.out = b.k2_32;
+    g.out = b.k2_16;
     g.out2 = b.vt2;
     g.nsplit = LTX_D;
     g.sat = sat;
     gemm16(c, mode, w->kv2, b.enc, S, LTX_D, LTX_EPI_QKV, g, st, "gemm:kv2");
-    qknorm16(c, mode, (const float*)b.q2_32, LTX_D, w->qn2.p, nullptr, nullptr, b.qh2, T, kAttnC, st);
-    qknorm16(c, mode, (const float*)b.k2_32, LTX_D, w->kn2.p, nullptr, nullptr, b.kh2, S, 1.0f, st);
+    qknorm16(c, mode, b.q2_16, LTX_D, w->qn2.p, nullptr, nullptr, b.qh2, T, kAttnC, st);
+    qknorm16(c, mode, b.k2_16, LTX_D, w->kn2.p, nullptr, nullptr, b.kh2, S, 1.0f, st);
+    stream_after(st, sd, c->side_ev[3]);  // glog2 ready
     attn16(c, mode, b.qh2, b.kh2, b.vt2, (const float*)b.glog2, b.o2, T, S, true, st, "attn:cross", sat);
     g = LtxGemmArgs{};
     g.out = b.x_ca;

@@ -83,6 +83,10 @@ struct ltx_ctx {
     // 3: software-pipelined 4 waves x 64 with LDS DMA (whole 32-key tiles; else 1),
     // 4: ping-pong 8 waves x 32 with LDS DMA (whole 64-key tiles; else 1)
     int attn_variant = 4;
+    // side stream of a forward: work off the main chain (gate logits, the
+    // cross-attention K/V) overlaps it, ordered by the events
+    hipStream_t side = nullptr;
+    hipEvent_t side_ev[4] = {};
     std::vector<hipModule_t> modules;
     std::map<std::string, hipFunction_t> fns;
     std::string err;

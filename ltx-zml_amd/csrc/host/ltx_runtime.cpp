@@ -170,6 +170,8 @@ int ltx_init(int device, ltx_ctx** out) {
                               : std::strcmp(e, "sp") == 0 ? 3
                               : std::strcmp(e, "pp") == 0 ? 4
                                                           : 1;
+        HIPC(hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking));  // default priority
+        for (auto& e : c->side_ev) HIPC(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         for (const unsigned char* co : {ltx_co_k_gemm, ltx_co_k_attn, ltx_co_k_norm, ltx_co_k_f32, ltx_co_k_core}) {
             hipModule_t m;
             HIPC(hipModuleLoadData(&m, co));
@@ -193,6 +195,9 @@ void ltx_destroy(ltx_ctx* c) {
         (void)hipEventDestroy(r.b);
     }
     for (auto e : c->ev_pool) (void)hipEventDestroy(e);
+    for (auto e : c->side_ev)
+        if (e) (void)hipEventDestroy(e);
+    if (c->side) (void)hipStreamDestroy(c->side);
     c->ws.free_();
     c->op_pairs.free_();
     c->op_q.free_();

@@ -121,6 +121,17 @@ extern "C" __global__ void __launch_bounds__(256) ltx_enc_f16(const LtxEncArgs a
 extern "C" __global__ void __launch_bounds__(256) ltx_enc_bf16(const LtxEncArgs a) { enc_body<1>(a); }
 extern "C" __global__ void __launch_bounds__(256) ltx_enc_f32(const LtxEncArgs a) { enc_body<2>(a); }
 
+// 8 consecutive 16-bit values (one 16-byte load) widened to f32 (exact).
+template <typename T>
+__device__ __forceinline__ void load8(const uint16_t* p, float* out) {
+    const u32x4 v = *(const u32x4*)p;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        out[2 * i] = Op<T>::to_f32((uint16_t)(v[i] & 0xffffu));
+        out[2 * i + 1] = Op<T>::to_f32((uint16_t)(v[i] >> 16));
+    }
+}
+
 // qk norm + RoPE (ltx/block.zig:32-34, 69-77, 214-226): y = rope(rms(x) * w).
 // Thread t owns head h = t / 8 and rotary slots f0 = 8 * (t % 8) .. f0 + 8, so
 // each RoPE pair (f, f + 64) lives in one thread. Output head-major [H][rows][HD].
@@ -130,16 +141,11 @@ __device__ void qknorm_body(const LtxQkNormArgs& a) {
     int row = blockIdx.x;
     if (row >= a.rows) return;
     int h = threadIdx.x >> 3, f0 = (threadIdx.x & 7) * 8;
-    const float* xr = a.x + (size_t)row * a.ldx + h * LTX_HD;
+    const uint16_t* xr = (const uint16_t*)a.x + (size_t)row * a.ldx + h * LTX_HD;
     float lo[8], hi[8];
     float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; j += 4) {
-        float4 p = *(const float4*)(xr + f0 + j);
-        float4 q = *(const float4*)(xr + 64 + f0 + j);
-        lo[j] = p.x; lo[j + 1] = p.y; lo[j + 2] = p.z; lo[j + 3] = p.w;
-        hi[j] = q.x; hi[j + 1] = q.y; hi[j + 2] = q.z; hi[j + 3] = q.w;
-    }
+    load8<T>(xr + f0, lo);
+    load8<T>(xr + 64 + f0, hi);
     // norm weights and RoPE rows do not depend on the row statistics: loaded
     // before the reduction so their latency overlaps it
     const float* wl = a.w + h * LTX_HD + f0;
@@ -202,12 +208,9 @@ __device__ void qknorm2_body(const LtxQkNorm2Args& a) {
     float lo[2][8], hi[2][8], cs[8], sn[8], wlo[2][8], whi[2][8];
 #pragma unroll
     for (int p = 0; p < 2; p++) {
-        const float* xr = a.x + (size_t)row * a.ldx + p * LTX_D + h * LTX_HD;
-#pragma unroll
-        for (int j = 0; j < 8; j += 4) {
-            *(float4*)(lo[p] + j) = *(const float4*)(xr + f0 + j);
-            *(float4*)(hi[p] + j) = *(const float4*)(xr + 64 + f0 + j);
-        }
+        const uint16_t* xr = (const uint16_t*)a.x + (size_t)row * a.ldx + p * LTX_D + h * LTX_HD;
+        load8<T>(xr + f0, lo[p]);
+        load8<T>(xr + 64 + f0, hi[p]);
         const float* wl = (p ? a.wk : a.wq) + h * LTX_HD + f0;
 #pragma unroll
         for (int j = 0; j < 8; j++) {

@@ -55,7 +55,7 @@ typedef struct {
 enum {
     LTX_EPI_STORE = 0,      // y = acc (+ bias); out f32 or 16-bit; optional GELU
     LTX_EPI_RESID_GATE = 1, // out32 = resid + (acc (+ bias)) * ada[igate]
-    LTX_EPI_QKV = 2,        // cols < nsplit: f32 [M][nsplit] (+bias); cols >= nsplit: 16-bit V^T [H][HD][M]
+    LTX_EPI_QKV = 2,        // cols < nsplit: 16-bit [M][nsplit] (+bias); cols >= nsplit: 16-bit V^T [H][HD][M]
 };
 
 // B operand kinds.
@@ -90,7 +90,7 @@ typedef struct {
 // Full-row qk RMSNorm (weighted, over all 4096 channels) + optional split-half
 // RoPE, writing the head-major 16-bit layout [H][rows][HD] the attention reads.
 typedef struct {
-    const float* x;     // [rows][ldx] f32 pre-norm projections
+    const void* x;      // [rows][ldx] pre-norm projections, in the 16-bit operand type
     const float* w;     // [D] norm weight (f32 copy of the bf16 tensor)
     const float* cos;   // [rows][H][64] or NULL (no RoPE)
     const float* sin;
@@ -104,7 +104,7 @@ typedef struct {
 // The self-attention's q and k rows of one token in one pass (the RoPE rows
 // read once): q = x[row][0 .. D), k = x[row][D .. 2D).
 typedef struct {
-    const float* x;     // [rows][ldx] f32, q | k
+    const void* x;      // [rows][ldx] q | k, in the 16-bit operand type
     const float* wq;    // [D] norm weights (f32)
     const float* wk;
     const float* cos;   // [rows][H][64]
