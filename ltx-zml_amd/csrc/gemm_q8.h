@@ -49,7 +49,7 @@
 // lgkmcnt for its LDS reads) followed by s_barrier. Each stage is its own
 // __shared__ object, so the compiler's alias tracking of LDS DMA sees that a
 // read of one stage does not depend on DMA into another and adds no
-// vmcnt(0) of its own. With PP, the two waves of a SIMD run half a tile
+// vmcnt(0) of its own. The two waves of a SIMD run half a tile
 // apart: while one multiplies, the other reads fragments, dequantises and
 // issues DMA.
 #pragma once
@@ -217,7 +217,7 @@ struct Q8Op<__bf16, false> : Q8Mfma<__bf16> {
 // Raw buffer descriptor word 3 for gfx9-family parts (untyped dword access).
 #define Q8_RSRC_W3 0x00020000
 
-template <typename T, bool SF32, int EPI, bool PP>
+template <typename T, bool SF32, int EPI>
 struct Q8Gemm {
     typedef Q8Op<T, SF32> QO;
     static constexpr int NI = 4, NJ = 2;
@@ -278,9 +278,9 @@ struct Q8Gemm {
         __builtin_amdgcn_sched_barrier(0);
         // ping-pong: the first DQ k-steps are dequantised in this (memory)
         // phase, so the MFMA phase opens with MFMAs; the rest interleave with it
-        constexpr int DQ = PP ? 2 : 0;
-        typename QO::V8 fb0[DQ > 0 ? DQ : 1][NJ];
-        if (PP) {
+        constexpr int DQ = 2;
+        typename QO::V8 fb0[DQ][NJ];
+        {
             __builtin_amdgcn_s_waitcnt(Q8_WAIT_LGKM0);
 #pragma unroll
             for (int t = 0; t < DQ; t++)
@@ -315,8 +315,8 @@ struct Q8Gemm {
                     acc[i][j] = QO::mfma(fa[i][t], fb[j], acc[i][j]);
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (PP) __builtin_amdgcn_s_setprio(0);
-        if (!PP || g == 0) wait_dma(more2);
+        __builtin_amdgcn_s_setprio(0);
+        if (g == 0) wait_dma(more2);
         __builtin_amdgcn_s_waitcnt(Q8_WAIT_LGKM0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
@@ -384,7 +384,7 @@ struct Q8Gemm {
             dma<1>(1);  // K is a multiple of 128: nk >= 2
             wait_dma(true);
             __builtin_amdgcn_s_barrier();
-            if (PP && g == 1) __builtin_amdgcn_s_barrier();
+            if (g == 1) __builtin_amdgcn_s_barrier();
             // Main loop: three tiles per trip, every one with a DMA two tiles
             // ahead; the last 2 to 4 tiles follow unrolled.
             const int trips = (nk - 2) / 3;
@@ -401,7 +401,7 @@ struct Q8Gemm {
                 if (k + 2 < nk) step<2>(k + 2, k + 4 < nk);
                 if (k + 3 < nk) step<0>(k + 3, false);
             }
-            if (PP && g == 0) __builtin_amdgcn_s_barrier();
+            if (g == 0) __builtin_amdgcn_s_barrier();
             // Every wave has passed its last barrier: no stage is read or DMA'd
             // any more, and each wave stages its epilogue in a private 9 KB patch.
             uint8_t* patch = w < 3 ? q8_sa0 + 9216 * w : w < 6 ? q8_sa1 + 9216 * (w - 3) : q8_sa2 + 9216 * (w - 6);
@@ -418,10 +418,6 @@ struct Q8Gemm {
 
 #define Q8_GEMM_KERNEL(NAME, T_, SF32_, EPI_)                                                \
     extern "C" __global__ void __launch_bounds__(512, 1) NAME(const LtxGemmArgs a) {         \
-        Q8Gemm<T_, SF32_, EPI_, false> k(a);                                                 \
-        k.run();                                                                             \
-    }                                                                                        \
-    extern "C" __global__ void __launch_bounds__(512, 1) NAME##_pp(const LtxGemmArgs a) {    \
-        Q8Gemm<T_, SF32_, EPI_, true> k(a);                                                  \
+        Q8Gemm<T_, SF32_, EPI_> k(a);                                                  \
         k.run();                                                                             \
     }

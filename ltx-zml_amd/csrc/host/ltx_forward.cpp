@@ -148,22 +148,20 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
     // 128, and byte offsets of A and W within 31 bits (32-bit buffer offsets)
     auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
     if ((mode == LTX_MODE_F16 || mode == LTX_MODE_BF16) && p.q8 && p.qflip && p.s2.p &&
-        c->gemm_q8 != 0 && p.K % 128 == 0 && (uint64_t)M * lda * 2 < (1ull << 31) && (uint64_t)p.N * p.K < (1ull << 31) && g.ldo % 8 == 0 &&
+        c->gemm_dma && p.K % 128 == 0 && (uint64_t)M * lda * 2 < (1ull << 31) && (uint64_t)p.N * p.K < (1ull << 31) && g.ldo % 8 == 0 &&
         al16(g.out) && al16(g.out2) && al16(g.resid) && al16(g.bias) && al16(g.ada.tstab) && al16(g.ada.sst)) {
         // (its epilogue moves 16-byte vectors: outputs, residual and bias 16-byte aligned)
         g.scales = p.s2.p;
-        std::snprintf(name, sizeof(name), "ltx_gemm_q8_%s%s%s%s", mode == LTX_MODE_BF16 ? "bf16_" : "",
+        std::snprintf(name, sizeof(name), "ltx_gemm_q8_%s%s%s", mode == LTX_MODE_BF16 ? "bf16_" : "",
                       p.scale_f16 ? "" : "s32_",
-                      epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv",
-                      c->gemm_q8 == 2 ? "_pp" : "");
+                      epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv");
         const int ntiles = g.tiles_m * g.tiles_n;
         c->launch(name, c->gemm_persistent ? std::min(ntiles, c->num_cu) : ntiles, 1, 1, 512, &g, st, label);
         return;
     }
-    std::snprintf(name, sizeof(name), "ltx_gemm_%s_%s_%s%s", msuffix(mode), bk,
-                  epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv",
-                  c->gemm_waves == 8 ? "_w8" : "");
-    c->launch(name, g.tiles_m * g.tiles_n, 1, 1, 64 * c->gemm_waves, &g, st, label);
+    std::snprintf(name, sizeof(name), "ltx_gemm_%s_%s_%s", msuffix(mode), bk,
+                  epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv");
+    c->launch(name, g.tiles_m * g.tiles_n, 1, 1, 512, &g, st, label);
 }
 
 static void gate16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M, float* out, hipStream_t st) {
@@ -196,29 +194,17 @@ static void attn16(ltx_ctx* c, int mode, const void* q, const void* k, const voi
     a.lq = lq;
     a.lkv = lkv;
     a.scale_log2 = q_scaled ? 1.0f : kAttnC;
-    int v = c->attn_variant;
-    a.q_tiles = (lq + 255) / 256;                    // 256 queries per workgroup
+    a.q_tiles = (lq + 255) / 256;  // 256 queries per workgroup
     char name[48];
-    if (v == 4) {
-        if (lkv % 64 == 0 && lkv >= 128) {  // ping-pong kernel: whole 64-key tiles, at least two
-            std::snprintf(name, sizeof(name), "ltx_attn_%s_pp%s", msuffix(mode), q_scaled ? "" : "_uq");
-            c->launch(name, a.q_tiles * LTX_H, 1, 1, 512, &a, st, label);
-            return;
-        }
-        v = 1;
+    if (c->attn_pp && lkv % 64 == 0 && lkv >= 128) {
+        // ping-pong kernel: whole 64-key tiles, at least two
+        std::snprintf(name, sizeof(name), "ltx_attn_%s_pp%s", msuffix(mode), q_scaled ? "" : "_uq");
+        c->launch(name, a.q_tiles * LTX_H, 1, 1, 512, &a, st, label);
+        return;
     }
-    if (v == 3) {
-        if (lkv % 32 == 0 && lkv >= 128) {  // software-pipelined kernel: whole 32-key tiles, at least four
-            std::snprintf(name, sizeof(name), "ltx_attn_%s_sp", msuffix(mode));
-            c->launch(name, a.q_tiles * LTX_H, 1, 1, 256, &a, st, label);
-            return;
-        }
-        v = 1;
-    }
-    const bool full = v != 0 && lkv % 64 == 0;       // key length a whole number of 64-key tiles
-    std::snprintf(name, sizeof(name), "ltx_attn_%s%s%s", msuffix(mode), v == 0 ? "" : v == 1 ? "_w8" : "_ps",
-                  full ? "_full" : "");
-    c->launch(name, a.q_tiles * LTX_H, 1, 1, v == 0 ? 256 : 512, &a, st, label);
+    // any key count: 8 waves of 32 queries (whole 64-key tiles: no masking)
+    std::snprintf(name, sizeof(name), "ltx_attn_%s_w8%s", msuffix(mode), lkv % 64 == 0 ? "_full" : "");
+    c->launch(name, a.q_tiles * LTX_H, 1, 1, 512, &a, st, label);
 }
 
 // f32-mode GEMM over rows [r0, r0 + N) of a (possibly fused) projection.
@@ -440,7 +426,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
 
 bool linear_q8_needs_scratch(const ltx_ctx* c, int N, int K, int mode) {
     (void)K;
-    return mode != LTX_MODE_F32 && c->gemm_q8 != 0 && N % 256 == 0;
+    return mode != LTX_MODE_F32 && c->gemm_dma && N % 256 == 0;
 }
 
 // ltx_op_linear_q8 / _noalloc: in the 16-bit modes with the LDS-DMA kernel the

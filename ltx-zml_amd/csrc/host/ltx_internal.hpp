@@ -73,16 +73,13 @@ struct ltx_block_weights {
 
 struct ltx_ctx {
     int device = 0;
-    // kernel variants: int8 GEMM (0: register-staged, 1: LDS-DMA, 2: LDS-DMA ping-pong),
-    // waves per workgroup of the register-staged GEMM (4 or 8), attention schedule
-    int gemm_q8 = 2;
-    int gemm_waves = 8;
+    // kernel selection: the int8 GEMM's LDS-DMA ping-pong kernel (true) or
+    // the register-staged one; the ping-pong attention for whole 64-key tiles
+    // (true) or the any-length kernel everywhere (both kept for testing)
+    bool gemm_dma = true;
     int num_cu = 256;             // compute units: the persistent GEMM's grid bound
     bool gemm_persistent = true;  // LDS-DMA GEMM: at most one workgroup per CU, looping over tiles
-    // attention: 0: 4 waves x 64 queries, 1: 8 waves x 32, 2: 8 waves, halves phase-shifted,
-    // 3: software-pipelined 4 waves x 64 with LDS DMA (whole 32-key tiles; else 1),
-    // 4: ping-pong 8 waves x 32 with LDS DMA (whole 64-key tiles; else 1)
-    int attn_variant = 4;
+    bool attn_pp = true;
     // side stream of a forward: work off the main chain (gate logits, the
     // cross-attention K/V) overlaps it, ordered by the events
     hipStream_t side = nullptr;

@@ -158,18 +158,12 @@ int ltx_init(int device, ltx_ctx** out) {
         HIPC(hipMemset(c->range_ctr.p, 0, 256));
         c->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
         // LTX_GEMM_GRID=tile: one workgroup per output tile instead of the
-        // persistent grid of one per CU (A/B timing)
+        // persistent grid of one per CU; LTX_GEMM_Q8=reg: the register-staged
+        // int8 GEMM everywhere; LTX_ATTN_VARIANT=w8: the any-length attention
+        // everywhere (the kernels each test exercises beside the defaults)
         if (const char* e = std::getenv("LTX_GEMM_GRID")) c->gemm_persistent = std::strcmp(e, "tile") != 0;
-        // variant overrides (used for A/B timing): 4 or 8 waves per workgroup
-        if (const char* e = std::getenv("LTX_GEMM_WAVES")) c->gemm_waves = std::atoi(e) == 4 ? 4 : 8;
-        if (const char* e = std::getenv("LTX_GEMM_Q8"))
-            c->gemm_q8 = std::strcmp(e, "reg") == 0 ? 0 : std::strcmp(e, "dma") == 0 ? 1 : 2;
-        if (const char* e = std::getenv("LTX_ATTN_VARIANT"))
-            c->attn_variant = std::strcmp(e, "w4") == 0   ? 0
-                              : std::strcmp(e, "ps") == 0 ? 2
-                              : std::strcmp(e, "sp") == 0 ? 3
-                              : std::strcmp(e, "pp") == 0 ? 4
-                                                          : 1;
+        if (const char* e = std::getenv("LTX_GEMM_Q8")) c->gemm_dma = std::strcmp(e, "reg") != 0;
+        if (const char* e = std::getenv("LTX_ATTN_VARIANT")) c->attn_pp = std::strcmp(e, "w8") != 0;
         HIPC(hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking));  // default priority
         for (auto& e : c->side_ev) HIPC(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         for (const unsigned char* co : {ltx_co_k_gemm, ltx_co_k_attn, ltx_co_k_norm, ltx_co_k_f32, ltx_co_k_core}) {

@@ -1,25 +1,22 @@
 // Blockwise online-softmax attention for gfx950 (the production attention of
 // ltx/block.zig:105-154, whileSdpaC), fused with the per-(token, head) gate
-// 2*sigmoid(glog) and the head merge (ltx/block.zig:237-242).
+// 2*sigmoid(glog) and the head merge (ltx/block.zig:237-242). Two kernels:
 //
-// A workgroup owns QT queries of one head; each wave owns QW = 32 * QB of
-// them. K and V^T are streamed through LDS in tiles of 64 keys (global ->
-// registers -> LDS, one barrier per tile). Scores are computed TRANSPOSED,
-// S^T = K . Q^T, and the output as O^T = V^T . P^T, with v_mfma_f32_32x32x16:
-// the query is then the MFMA column index, so lane l always holds query
-// l % 32 — its running max m, partial sum l and its O^T column stay
-// lane-local, and only the tile max needs one exchange with lane l ^ 32.
-// The P^T operand comes straight from the S^T accumulators (no LDS round
-// trip): within every 16-key chunk the keys are consumed in the order 0-3,
-// 8-11, 4-7, 12-15, which is the order the accumulator layout hands them to
-// each lane, and the V^T tile is stored in LDS permuted the same way.
+// - ltx_attn_{f16,bf16}_pp (the ping-pong kernel, below): whole 64-key tiles
+//   (lkv % 64 == 0, at least two), K and V^T streamed global -> LDS by DMA;
+//   the block's self- and cross-attention take it;
+// - ltx_attn_{f16,bf16}_w8[_full] (any key count): 8 waves of 32 queries, K
+//   and V^T staged through registers into LDS, keys past lkv masked.
 //
-// Eight-wave variant (two waves per SIMD) runs the two halves of the
-// workgroup half a tile apart: waves 0-3 do S(j), softmax(j), PV(j) while
-// waves 4-7 do softmax(j-1), PV(j-1), S(j). Within one barrier interval one
-// half issues MFMAs while the other half runs the softmax VALU work, instead
-// of both contending for the same unit at the same time. This needs the V
-// tile of j-1 alive during iteration j: K/V use three LDS buffers.
+// Both compute the scores TRANSPOSED, S^T = K . Q^T, and the output as
+// O^T = V^T . P^T, with v_mfma_f32_32x32x16: the query is then the MFMA
+// column index, so lane l always holds query l % 32 — its running max m,
+// partial sum l and its O^T column stay lane-local, and only the tile max
+// needs one exchange with lane l ^ 32. The P^T operand comes straight from
+// the S^T accumulators (no LDS round trip): within every 16-key chunk the
+// keys are consumed in the order 0-3, 8-11, 4-7, 12-15, which is the order
+// the accumulator layout hands them to each lane, and the K (or V^T) tile is
+// stored in LDS permuted to match.
 //
 // Statistics are f32. Softmax uses exp2 with the 1/sqrt(128) scale folded
 // into the exponent (s * C - m * C, C = scale * log2 e); m starts at -FLT_MAX
@@ -34,14 +31,14 @@
 #define RESCALE_LOG2 8.0f  // rescale threshold, in log2 units of p
 
 // QB: 32-query column blocks per wave. NW: waves per workgroup. FULL: lkv is
-// a multiple of 64 (no tail handling, no masking). PS: phase-shifted halves.
-template <typename T, int QB, bool FULL, int NW, bool PS>
+// a multiple of 64 (no tail handling, no masking).
+template <typename T, int QB, bool FULL, int NW>
 __device__ void attn_body(const LtxAttnArgs& a) {
     typedef typename Op<T>::v8 v8;
     constexpr int NT = 64 * NW;         // threads per workgroup
     constexpr int QT = NW * 32 * QB;    // queries per workgroup
     constexpr int QW = 32 * QB;         // queries per wave
-    constexpr int NBUF = PS ? 3 : 2;    // LDS tile buffers
+    constexpr int NBUF = 2;             // LDS tile buffers
     __shared__ __attribute__((aligned(16))) uint16_t sK[NBUF][KT * KROW];
     __shared__ __attribute__((aligned(16))) uint16_t sV[NBUF][LTX_HD * VROW];
 
@@ -213,41 +210,19 @@ __device__ void attn_body(const LtxAttnArgs& a) {
 
     STile s;
     PTile pf;
-    if (!PS || w < NW / 2) {
-        // in-phase: S(j), softmax(j), PV(j)
-        for (int j = 0; j + 1 < ntiles; j++) {
-            gload((j + 1) * KT);
-            scores(j % NBUF, s);
-            softmax(s, pf, j * KT, false);
-            pv(j % NBUF, pf);
-            sstore((j + 1) % NBUF);
-            __syncthreads();
-        }
-        const int jl = ntiles - 1;
-        scores(jl % NBUF, s);
-        softmax(s, pf, jl * KT, true);
-        pv(jl % NBUF, pf);
-    } else {
-        // half a tile behind: softmax(j-1), PV(j-1), S(j)
-        for (int j = 0; j + 1 < ntiles; j++) {
-            gload((j + 1) * KT);
-            if (j > 0) {
-                softmax(s, pf, (j - 1) * KT, false);
-                pv((j - 1) % NBUF, pf);
-            }
-            scores(j % NBUF, s);
-            sstore((j + 1) % NBUF);
-            __syncthreads();
-        }
-        const int jl = ntiles - 1;
-        if (jl > 0) {
-            softmax(s, pf, (jl - 1) * KT, false);
-            pv((jl - 1) % NBUF, pf);
-        }
-        scores(jl % NBUF, s);
-        softmax(s, pf, jl * KT, true);
-        pv(jl % NBUF, pf);
+    // S(j), softmax(j), PV(j)
+    for (int j = 0; j + 1 < ntiles; j++) {
+        gload((j + 1) * KT);
+        scores(j % NBUF, s);
+        softmax(s, pf, j * KT, false);
+        pv(j % NBUF, pf);
+        sstore((j + 1) % NBUF);
+        __syncthreads();
     }
+    const int jl = ntiles - 1;
+    scores(jl % NBUF, s);
+    softmax(s, pf, jl * KT, true);
+    pv(jl % NBUF, pf);
 
     // out[q][h * 128 + d] = O^T[d][q] / l * 2 sigmoid(glog[q][h])
     uint16_t* out = (uint16_t*)a.out;
@@ -275,383 +250,29 @@ __device__ void attn_body(const LtxAttnArgs& a) {
     range_report(a.sat, bad);
 }
 
-#define ATTN_KERNEL(NAME, T, QB, FULL, NW, PS)                                                      \
+#define ATTN_KERNEL(NAME, T, QB, FULL, NW)                                                          \
     extern "C" __global__ void __launch_bounds__(64 * NW, 1) NAME(const LtxAttnArgs a) {           \
-        attn_body<T, QB, FULL, NW, PS>(a);                                                          \
+        attn_body<T, QB, FULL, NW>(a);                                                              \
     }
 
-ATTN_KERNEL(ltx_attn_f16, _Float16, 2, false, 4, false)
-ATTN_KERNEL(ltx_attn_bf16, __bf16, 2, false, 4, false)
-ATTN_KERNEL(ltx_attn_f16_w8, _Float16, 1, false, 8, false)
-ATTN_KERNEL(ltx_attn_bf16_w8, __bf16, 1, false, 8, false)
-ATTN_KERNEL(ltx_attn_f16_w8_full, _Float16, 1, true, 8, false)
-ATTN_KERNEL(ltx_attn_bf16_w8_full, __bf16, 1, true, 8, false)
-ATTN_KERNEL(ltx_attn_f16_ps, _Float16, 1, false, 8, true)
-ATTN_KERNEL(ltx_attn_bf16_ps, __bf16, 1, false, 8, true)
-ATTN_KERNEL(ltx_attn_f16_ps_full, _Float16, 1, true, 8, true)
-ATTN_KERNEL(ltx_attn_bf16_ps_full, __bf16, 1, true, 8, true)
+// the any-length kernels: 8 waves of 32 queries, registers-staged K/V
+ATTN_KERNEL(ltx_attn_f16_w8, _Float16, 1, false, 8)
+ATTN_KERNEL(ltx_attn_bf16_w8, __bf16, 1, false, 8)
+ATTN_KERNEL(ltx_attn_f16_w8_full, _Float16, 1, true, 8)
+ATTN_KERNEL(ltx_attn_bf16_w8_full, __bf16, 1, true, 8)
 
 // ---------------------------------------------------------------------------
-// Software-pipelined kernel for whole 32-key tiles (lkv % 32 == 0, at least
-// four tiles): 4 waves of 64 queries each (two 32-query column blocks), one
-// wave per SIMD with the whole register file. Iteration j issues the MFMAs
-// of S(j+1) and of PV(j-1) and, independent of both, the softmax VALU work
-// of tile j: phase A pairs S(j+1) with the softmax of query block 0, phase B
-// pairs PV(j-1) with query block 1, so the SIMD's matrix core and vector ALU
-// run at the same time within one wave. The output rescale a moving max calls
-// for is applied after PV(j-1), before PV(j) adds in the next iteration.
-//
-// K and V^T tiles go global -> LDS by DMA (buffer_load ... lds) into four
-// stages each: iteration j issues K(j+4) and V(j+2) and, before its closing
-// barrier, waits for K(j+2) and V(j) (two iterations of latency cover). Every
-// stage is its own __shared__ object, so the compiler sees that reads of one
-// stage do not depend on DMA into another.
-//
-// K rows are stored permuted within each group of 16 keys (LDS row r holds
-// key r with bits 2 and 3 swapped: rows 0-3, 4-7, 8-11, 12-15 hold keys 0-3,
-// 8-11, 4-7, 12-15). The S^T accumulator rows a lane holds are then, in
-// order, 8 consecutive keys per 16-key step, exactly the P^T operand of the
-// PV MFMA, and V^T stays in natural key order. 16-byte chunks are XOR
-// swizzled: K row r (256 B) chunk c in slot c ^ (r & 15), V^T row d (64 B)
-// chunk c in slot c ^ ((d >> 2) & 3), so each 16-lane group of a
-// ds_read_b128 covers all 64 banks once.
+// Helpers of the LDS-DMA kernel below.
 typedef __attribute__((address_space(3))) void* attn_lds_ptr;
 #define ASP_WAIT_VM(n) ((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
 #define ASP_WAIT_LGKM0 (15 | (3 << 14) | (7 << 4))
 #define ASP_RSRC_W3 0x00020000
-#define ASP_KT 32  // keys per tile
-
-__shared__ __attribute__((aligned(1024))) uint8_t asp_k0[8192];
-__shared__ __attribute__((aligned(1024))) uint8_t asp_k1[8192];
-__shared__ __attribute__((aligned(1024))) uint8_t asp_k2[8192];
-__shared__ __attribute__((aligned(1024))) uint8_t asp_k3[8192];
-__shared__ __attribute__((aligned(1024))) uint8_t asp_v0[8192];
-__shared__ __attribute__((aligned(1024))) uint8_t asp_v1[8192];
-__shared__ __attribute__((aligned(1024))) uint8_t asp_v2[8192];
-__shared__ __attribute__((aligned(1024))) uint8_t asp_v3[8192];
-
-template <int S>
-__device__ __forceinline__ uint8_t* asp_k() {
-    return S == 0 ? asp_k0 : S == 1 ? asp_k1 : S == 2 ? asp_k2 : asp_k3;
-}
-template <int S>
-__device__ __forceinline__ uint8_t* asp_v() {
-    return S == 0 ? asp_v0 : S == 1 ? asp_v1 : S == 2 ? asp_v2 : asp_v3;
-}
 
 // max of x and the same register in the other half of the wave (lane ^ 32)
 __device__ __forceinline__ float asp_xhalf_max(float x) {
     const uint32_t u = __builtin_bit_cast(uint32_t, x);
     const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
     return fmaxf(x, fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])));
-}
-
-template <typename T>
-struct AttnSP {
-    typedef typename Op<T>::v8 v8;
-    static constexpr int QB = 2;
-    const LtxAttnArgs& a;
-    __amdgpu_buffer_rsrc_t rk, rv;
-    uint32_t gk[2], gv[2];  // per-lane DMA source offsets in tile 0
-    int lw;                 // this wave's 2 KB slice of a stage
-    uint32_t ok[8];         // K fragment offsets per 16-dim step c
-    uint32_t ov[2];         // V^T fragment offsets per 16-key step kc (db adds 2048)
-    v8 qf[QB][8];
-    f32x16 o[QB][4];
-    f32x16 s[2][QB];  // [parity][qb]
-    v8 pf[2][QB][2];  // [parity][qb][kc]
-    float m[QB], l[QB], corr[QB];
-    bool resc;
-    float C;
-    int nt;
-
-    __device__ __forceinline__ AttnSP(const LtxAttnArgs& args) : a(args) {}
-
-    template <int S>
-    __device__ __forceinline__ void dma_k(int t) {
-        uint8_t* d = asp_k<S>() + lw;
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (attn_lds_ptr)(d + 1024 * i), 16, gk[i], t * 8192, 0, 0);
-    }
-    template <int S>
-    __device__ __forceinline__ void dma_v(int t) {
-        uint8_t* d = asp_v<S>() + lw;
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (attn_lds_ptr)(d + 1024 * i), 16, gv[i], t * 64, 0, 0);
-    }
-
-    // S^T(tile in K stage KS) into s[P]
-    template <int KS, int P>
-    __device__ __forceinline__ void scores() {
-        const uint8_t* sk = asp_k<KS>();
-#pragma unroll
-        for (int qb = 0; qb < QB; qb++) s[P][qb] = f32x16{0};
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const v8 kf = __builtin_bit_cast(v8, *(const u32x4*)(sk + ok[c]));
-#pragma unroll
-            for (int qb = 0; qb < QB; qb++) s[P][qb] = Op<T>::mfma32(kf, qf[qb][c], s[P][qb]);
-        }
-    }
-
-    // online softmax of query block qb of s[P] -> pf[P][qb]; a moving max
-    // leaves corr[qb] / resc for the output rescale after this iteration's PV
-    template <int P, int qb>
-    __device__ __forceinline__ void softmax() {
-        float mx = s[P][qb][0];
-#pragma unroll
-        for (int r = 1; r < 16; r++) mx = fmaxf(mx, s[P][qb][r]);
-        mx = asp_xhalf_max(mx);
-        // branch-free (selects), so the MFMAs of this phase can be scheduled
-        // around the softmax: the max moves only when some query of the wave
-        // exceeds it by the threshold
-        const bool up = __builtin_amdgcn_ballot_w64(mx > m[qb] + RESCALE_LOG2 / C) != 0;
-        const float mn = up ? fmaxf(m[qb], mx) : m[qb];
-        corr[qb] = __builtin_amdgcn_exp2f((m[qb] - mn) * C);
-        m[qb] = mn;
-        l[qb] *= corr[qb];
-        resc = resc || up;
-        const float mc = m[qb] * C;
-        float ps = 0.f;
-#pragma unroll
-        for (int kc = 0; kc < 2; kc++) {
-            float p[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[P][qb][8 * kc + e], C, -mc));
-            const u32x4 pk4 = {Op<T>::cvt2(p[0], p[1]), Op<T>::cvt2(p[2], p[3]), Op<T>::cvt2(p[4], p[5]),
-                               Op<T>::cvt2(p[6], p[7])};
-#pragma unroll
-            for (int e = 0; e < 4; e++) ps = Op<T>::sum2(pk4[e], ps);
-            pf[P][qb][kc] = __builtin_bit_cast(v8, pk4);
-        }
-        l[qb] += ps;
-    }
-
-    // O^T += V^T(stage VS) . P^T(pf[P])
-    template <int VS, int P>
-    __device__ __forceinline__ void pv() {
-        const uint8_t* sv = asp_v<VS>();
-#pragma unroll
-        for (int kc = 0; kc < 2; kc++) {
-#pragma unroll
-            for (int db = 0; db < 4; db++) {
-                const v8 vf = __builtin_bit_cast(v8, *(const u32x4*)(sv + ov[kc] + 2048 * db));
-#pragma unroll
-                for (int qb = 0; qb < QB; qb++) o[qb][db] = Op<T>::mfma32(vf, pf[P][qb][kc], o[qb][db]);
-            }
-        }
-    }
-
-    // Empty asm uses of this iteration's softmax results: they must exist
-    // before the (rarely taken) rescale branch, so no pass sinks the softmax
-    // below it and out of the phases it is interleaved with.
-    template <int P>
-    __device__ __forceinline__ void pin_softmax() {
-#pragma unroll
-        for (int qb = 0; qb < QB; qb++) {
-#pragma unroll
-            for (int kc = 0; kc < 2; kc++) asm volatile("" ::"v"(__builtin_bit_cast(u32x4, pf[P][qb][kc])));
-            asm volatile("" ::"v"(l[qb]), "v"(m[qb]), "v"(corr[qb]));
-        }
-    }
-
-    __device__ __forceinline__ void rescale() {
-        if (resc) {
-#pragma unroll
-            for (int qb = 0; qb < QB; qb++)
-#pragma unroll
-                for (int db = 0; db < 4; db++) o[qb][db] *= corr[qb];
-        }
-    }
-
-    // Interleave hint for one phase: fragment reads run three MFMA pairs
-    // ahead, and each pair of MFMAs is followed by two exp2 and five other
-    // VALU instructions of the softmax (masks: 0x100 DS read, 0x008 MFMA,
-    // 0x400 transcendental, 0x002 VALU).
-    __device__ __forceinline__ void interleave() {
-        __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-            if (i < 5) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-    }
-
-    __device__ __forceinline__ void wait_vm(int n) {
-        switch (n) {
-            case 8: __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(8)); break;
-            case 6: __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(6)); break;
-            case 4: __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(4)); break;
-            case 2: __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(2)); break;
-            default: __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(0)); break;
-        }
-    }
-    // DMA instructions issued by iteration j (K(j+4), V(j+2)); j = -1 and -2
-    // stand for the prologue groups (V(1), K(3)) and (V(0), K(2))
-    __device__ __forceinline__ int ops(int j) const {
-        return (j + 4 < nt ? 2 : 0) + (j + 2 < nt ? 2 : 0);
-    }
-
-    // Iteration j (J = j mod 4): S(j+1) | softmax(j); DMA K(j+4), V(j+2);
-    // PV(j-1) | softmax(j); rescale; wait for K(j+2) and V(j); barrier.
-    template <int J>
-    __device__ __forceinline__ void iter(int j, bool dk, bool dv, bool ds, bool dp, int nwait) {
-        constexpr int P = J % 2;
-        __builtin_amdgcn_sched_barrier(0);
-        resc = false;
-        // phase A: S(j+1) on the matrix core, softmax of query block 0 on the VALU
-        if (ds) scores<(J + 1) % 4, P ^ 1>();
-        softmax<P, 0>();
-        interleave();
-        __builtin_amdgcn_sched_barrier(0);
-        if (dk) dma_k<J>(j + 4);
-        if (dv) dma_v<(J + 2) % 4>(j + 2);
-        __builtin_amdgcn_sched_barrier(0);
-        // phase B: PV(j-1) on the matrix core, softmax of query block 1 on the VALU
-        if (dp) pv<(J + 3) % 4, P ^ 1>();
-        softmax<P, 1>();
-        interleave();
-        __builtin_amdgcn_sched_barrier(0);
-        pin_softmax<P>();
-        rescale();
-        __builtin_amdgcn_sched_barrier(0);
-        wait_vm(nwait);
-        __builtin_amdgcn_s_waitcnt(ASP_WAIT_LGKM0);
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-    }
-
-    template <int J>
-    __device__ __forceinline__ void tail_iter(int j) {
-        if (j < nt) iter<J>(j, j + 4 < nt, j + 2 < nt, j + 1 < nt, true, ops(j - 1) + ops(j));
-    }
-
-    template <int J>
-    __device__ __forceinline__ void last_pv() {
-        pv<(J + 3) % 4, (J + 1) % 2>();  // PV(nt - 1) with nt % 4 == J
-    }
-
-    __device__ __forceinline__ void run() {
-        const int tid = threadIdx.x, lane = tid & 63;
-        const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-        const int nblk = a.q_tiles * LTX_H;
-        int t = blockIdx.x;
-        if ((nblk & 7) == 0) t = (t & 7) * (nblk >> 3) + (t >> 3);
-        const int h = t / a.q_tiles, qt = t - h * a.q_tiles;
-        const int q0 = qt * 256 + w * 64;
-        const int lq = a.lq, lkv = a.lkv;
-        nt = lkv / ASP_KT;
-        C = a.scale_log2;
-        const uint16_t* Q = (const uint16_t*)a.q + (size_t)h * lq * LTX_HD;
-        rk = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint16_t*)a.k + (size_t)h * lkv * LTX_HD), 0,
-                                               lkv * LTX_HD * 2, ASP_RSRC_W3);
-        rv = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint16_t*)a.vt + (size_t)h * LTX_HD * lkv), 0,
-                                               lkv * LTX_HD * 2, ASP_RSRC_W3);
-        lw = 2048 * w;
-        // DMA sources: K instruction i of wave w fills LDS rows 4 (2 w + i) ..
-        // +3 (16 lanes a row); V^T rows 16 (2 w + i) .. +15 (4 lanes a row)
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int r = 4 * (2 * w + i) + (lane >> 4);  // LDS row = key slot
-            const int key = (r & ~15) | (r & 3) | ((r & 4) << 1) | ((r & 8) >> 1);
-            const int c = (lane & 15) ^ (r & 15);
-            gk[i] = (uint32_t)key * 256u + 16u * c;
-            const int d = 16 * (2 * w + i) + (lane >> 2);
-            const int cv = (lane & 3) ^ ((d >> 2) & 3);
-            gv[i] = (uint32_t)d * (uint32_t)lkv * 2u + 16u * cv;
-        }
-        {
-            const int hh = lane >> 5, r = lane & 31;
-#pragma unroll
-            for (int c = 0; c < 8; c++) ok[c] = r * 256 + 16 * ((2 * c + hh) ^ (r & 15));
-#pragma unroll
-            for (int kc = 0; kc < 2; kc++) ov[kc] = r * 64 + 16 * ((2 * kc + hh) ^ ((r >> 2) & 3));
-#pragma unroll
-            for (int qb = 0; qb < QB; qb++) {
-                const int q = min(q0 + 32 * qb + r, lq - 1);
-#pragma unroll
-                for (int c = 0; c < 8; c++)
-                    qf[qb][c] = __builtin_bit_cast(v8, *(const u32x4*)(Q + (size_t)q * LTX_HD + 16 * c + 8 * hh));
-            }
-        }
-#pragma unroll
-        for (int qb = 0; qb < QB; qb++) {
-#pragma unroll
-            for (int db = 0; db < 4; db++) o[qb][db] = f32x16{0};
-            m[qb] = -3.402823466e38f;
-            l[qb] = 0.f;
-        }
-        // prologue (nt >= 4): K(0), K(1) | V(0), K(2) | V(1), K(3); S(0) once
-        // K(0) and K(1) have landed
-        dma_k<0>(0);
-        dma_k<1>(1);
-        dma_v<0>(0);
-        dma_k<2>(2);
-        dma_v<1>(1);
-        dma_k<3>(3);
-        wait_vm(8);
-        __builtin_amdgcn_s_barrier();
-        scores<0, 0>();
-        __builtin_amdgcn_s_waitcnt(ASP_WAIT_LGKM0);
-        __builtin_amdgcn_s_barrier();  // every wave is done with stage K0 before iteration 0 refills it
-        iter<0>(0, 4 < nt, 2 < nt, true, false, ops(-1) + ops(0));
-        // main loop: four iterations a trip, every DMA present (j + 3 + 4 < nt)
-        int j = 1;
-        for (; j + 7 < nt; j += 4) {
-            iter<1>(j, true, true, true, true, 8);
-            iter<2>(j + 1, true, true, true, true, 8);
-            iter<3>(j + 2, true, true, true, true, 8);
-            iter<0>(j + 3, true, true, true, true, 8);
-        }
-        // tail: at most 7 more iterations (j = 1 mod 4 here)
-        tail_iter<1>(j);
-        tail_iter<2>(j + 1);
-        tail_iter<3>(j + 2);
-        tail_iter<0>(j + 3);
-        tail_iter<1>(j + 4);
-        tail_iter<2>(j + 5);
-        tail_iter<3>(j + 6);
-        switch (nt % 4) {
-            case 0: last_pv<0>(); break;
-            case 1: last_pv<1>(); break;
-            case 2: last_pv<2>(); break;
-            default: last_pv<3>(); break;
-        }
-        // out[q][h * 128 + d] = O^T[d][q] / l * 2 sigmoid(glog[q][h])
-        uint16_t* out = (uint16_t*)a.out;
-        const int hh = lane >> 5;
-#pragma unroll
-        for (int qb = 0; qb < QB; qb++) {
-            const float lt = l[qb] + __shfl_xor(l[qb], 32, 64);
-            const int q = q0 + 32 * qb + (lane & 31);
-            if (q >= lq) continue;
-            const float g = a.glog ? 2.0f * sigmoid_f(a.glog[(size_t)q * LTX_H + h]) : 1.0f;
-            const float sc = g / lt;
-#pragma unroll
-            for (int db = 0; db < 4; db++) {
-#pragma unroll
-                for (int rg = 0; rg < 4; rg++) {
-                    const int d = 32 * db + 8 * rg + 4 * hh;
-                    const u32x2 pk2 = {Op<T>::cvt2(o[qb][db][4 * rg] * sc, o[qb][db][4 * rg + 1] * sc),
-                                       Op<T>::cvt2(o[qb][db][4 * rg + 2] * sc, o[qb][db][4 * rg + 3] * sc)};
-                    *(u32x2*)(out + (size_t)q * LTX_D + h * LTX_HD + d) = pk2;
-                }
-            }
-        }
-    }
-};
-
-extern "C" __global__ void __launch_bounds__(256, 1) ltx_attn_f16_sp(const LtxAttnArgs a) {
-    AttnSP<_Float16> k(a);
-    k.run();
-}
-extern "C" __global__ void __launch_bounds__(256, 1) ltx_attn_bf16_sp(const LtxAttnArgs a) {
-    AttnSP<__bf16> k(a);
-    k.run();
 }
 
 // ---------------------------------------------------------------------------

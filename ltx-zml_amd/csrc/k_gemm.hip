@@ -151,10 +151,7 @@ __device__ void gemm_body(const LtxGemmArgs& a) {
 }
 
 #define GEMM_KERNEL(NAME, T, BK_, EPI_)                                                        \
-    extern "C" __global__ void __launch_bounds__(256, 1) NAME(const LtxGemmArgs a) {           \
-        gemm_body<T, BK_, EPI_, 4>(a);                                                         \
-    }                                                                                          \
-    extern "C" __global__ void __launch_bounds__(512, 1) NAME##_w8(const LtxGemmArgs a) {      \
+    extern "C" __global__ void __launch_bounds__(512, 1) NAME(const LtxGemmArgs a) {           \
         gemm_body<T, BK_, EPI_, 8>(a);                                                         \
     }
 
@@ -175,9 +172,8 @@ GEMM_KERNEL(ltx_gemm_bf16_i8f16_qkv, __bf16, LTX_B_I8_F16S, LTX_EPI_QKV)
 GEMM_KERNEL(ltx_gemm_bf16_w16_store, __bf16, LTX_B_W16, LTX_EPI_STORE)
 GEMM_KERNEL(ltx_gemm_bf16_w16_resid, __bf16, LTX_B_W16, LTX_EPI_RESID_GATE)
 
-// LDS-DMA W8A16 kernels: ltx_gemm_q8_[bf16_][s32_]{store,resid,qkv}[_pp] for
-// f16 (bf16_: bf16) operands with f16 (s32_: f32) scales; _pp is the
-// ping-pong schedule.
+// LDS-DMA W8A16 kernels (ping-pong schedule): ltx_gemm_q8_[bf16_][s32_]{store,
+// resid,qkv} for f16 (bf16_: bf16) operands with f16 (s32_: f32) scales.
 Q8_GEMM_KERNEL(ltx_gemm_q8_store, _Float16, false, LTX_EPI_STORE)
 Q8_GEMM_KERNEL(ltx_gemm_q8_resid, _Float16, false, LTX_EPI_RESID_GATE)
 Q8_GEMM_KERNEL(ltx_gemm_q8_qkv, _Float16, false, LTX_EPI_QKV)
