@@ -275,6 +275,11 @@ def denoise_bench(args) -> int:
     return 0
 
 
+# launch labels of one block forward (a label covers every launch whose name
+# contains it): ms per launch at T = 28,672, ms per forward at T = 1,024
+KERNEL_LABELS = ("attn:self", "attn:cross", "gemm:qkv1", "gemm:o1", "gemm:q2", "gemm:kv2", "gemm:o2", "gemm:ff1",
+                 "gemm:ff2", "ltx_norm_mod", "ltx_qknorm", "ltx_gate", "ltx_enc", "splitk_reduce")
+
 GEMM_SWEEP = [(4096, 4096, 4096), (28672, 4096, 4096), (28672, 4096, 16384), (28672, 16384, 4096)]  # M, K, N
 ATTN_SWEEP = [(4096, 4096), (16384, 16384), (28672, 28672), (28672, 256)]  # Lq, Lkv
 
@@ -444,8 +449,7 @@ def main() -> int:
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
     per = {}
-    for lab in ("attn:self", "attn:cross", "gemm:qkv1", "gemm:o1", "gemm:q2", "gemm:kv2", "gemm:o2", "gemm:ff1",
-                "gemm:ff2", "ltx_norm_mod", "ltx_qknorm", "ltx_gate", "ltx_enc"):
+    for lab in KERNEL_LABELS:
         tot, n = ctx.profile_read(lab)
         per[lab] = round(tot / max(n, 1), 4)
     ctx.profile(False)
@@ -504,6 +508,12 @@ def main() -> int:
     e1.record(stream)
     torch.cuda.synchronize()
     res["t1024_block_ms"] = round(e0.elapsed_time(e1) / 20, 4)
+    ctx.profile(True)  # per-kernel times of the same forward, in a separate pass
+    ctx.profile_reset()
+    for _ in range(5):
+        step0()
+    res["t1024_kernel_ms"] = {lab: round(ctx.profile_read(lab)[0] / 5, 4) for lab in KERNEL_LABELS}
+    ctx.profile(False)
     log(f"bench: T=1024 block {res['t1024_block_ms']:.3f} ms")
     w0.free()
     if not args.no_denoise:

@@ -197,3 +197,29 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
     }
     range_report(a.sat, bad);
 }
+
+// Split-K partial sums: one wave's (32 NI) x (32 NJ) f32 accumulators to
+// part[m][n] (row stride N), through the same wave-private LDS patch as the
+// epilogues so that every store is 16 contiguous bytes of a row.
+template <int NI, int NJ>
+__device__ __forceinline__ void gemm_store_partial(const f32x16 (&acc)[NI][NJ], float* patch, float* part, int M,
+                                                   int N, int mw, int nw) {
+    constexpr int WN = 32 * NJ, LD = WN + 8;
+    constexpr int LPR = WN / 4, RPP = 64 / LPR;  // lanes per row, rows per pass
+    const int lane = threadIdx.x & 63;
+    const int c4 = 4 * (lane % LPR), r0 = lane / LPR;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int mb = mw + 32 * i;
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                patch[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * LD + 32 * j + (lane & 31)] = acc[i][j][r];
+#pragma unroll
+        for (int p = 0; p < 32 / RPP; p++) {
+            const int rr = r0 + RPP * p, m = mb + rr;
+            if (m < M) *(f32x4*)(part + (size_t)m * N + nw + c4) = *(const f32x4*)(patch + rr * LD + c4);
+        }
+    }
+}

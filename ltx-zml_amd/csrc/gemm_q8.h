@@ -333,12 +333,17 @@ struct Q8Gemm {
         const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
         g = w >> 2;
         const int q = w & 3;
-        nk = a.K / 64;
-        ng = a.K / LTX_GROUP;
+        // split-K: each work item is one output tile and one of ksplit slices
+        // of K (kc = K / ksplit, a multiple of 128); offsets below add the
+        // slice's first k
+        const int ks_n = a.ksplit > 1 ? a.ksplit : 1;
+        const int kc = a.K / ks_n;
+        nk = kc / 64;
+        ng = kc / LTX_GROUP;
         ra_ = __builtin_amdgcn_make_buffer_rsrc((void*)a.a, 0, (int)((uint32_t)a.M * (uint32_t)a.lda * 2u), Q8_RSRC_W3);
         rb_ = __builtin_amdgcn_make_buffer_rsrc((void*)a.b, 0, (int)((uint32_t)a.N * (uint32_t)a.K), Q8_RSRC_W3);
-        rs_ = __builtin_amdgcn_make_buffer_rsrc((void*)a.scales, 0, (int)((uint32_t)ng * (uint32_t)a.N * 4u),
-                                                Q8_RSRC_W3);
+        rs_ = __builtin_amdgcn_make_buffer_rsrc((void*)a.scales, 0,
+                                                (int)((uint32_t)(a.K / LTX_GROUP) * (uint32_t)a.N * 4u), Q8_RSRC_W3);
         la = 4096 * w;
         lb = 2048 * w;
         // fragment reads: A row 128 g + 32 i + lane % 32, chunks 4 h + t;
@@ -350,10 +355,12 @@ struct Q8Gemm {
 #pragma unroll
             for (int c = 0; c < 2; c++) offb[c] = (64 * q + r) * 64 + 16 * ((2 * h + c) ^ ((r >> 2) & 3));
         }
-        const int ntiles = a.tiles_m * a.tiles_n;
-        for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-            const TileIdx ti = tile_of(tile, a.tiles_m, a.tiles_n);
+        const int ntiles = a.tiles_m * a.tiles_n * ks_n;
+        for (int item = blockIdx.x; item < ntiles; item += gridDim.x) {
+            const int ks = item % ks_n;
+            const TileIdx ti = tile_of(item / ks_n, a.tiles_m, a.tiles_n);
             const int m0 = ti.tm * 256, n0 = ti.tn * 256;
+            const uint32_t k0 = (uint32_t)(ks * kc);  // first k of this slice
             // DMA sources. A: instruction i of wave w fills rows 8 (4 w + i) ..
             // +7, 8 lanes a row; W: rows 16 (2 w + i) .. +15, 4 lanes a row.
 #pragma unroll
@@ -361,15 +368,15 @@ struct Q8Gemm {
                 const int tr = 8 * (4 * w + i) + (lane >> 3);  // row within the tile
                 const int c = (lane & 7) ^ ((tr >> 1) & 7);
                 const int row = min(m0 + tr, a.M - 1);
-                ga[i] = (uint32_t)row * (uint32_t)a.lda * 2u + 16u * c;
+                ga[i] = (uint32_t)row * (uint32_t)a.lda * 2u + 2u * k0 + 16u * c;
             }
             {
                 const int nr = lane >> 2, nc = (lane & 3) ^ ((lane >> 4) & 3);
 #pragma unroll
                 for (int i = 0; i < 2; i++)
-                    gb[i] = (uint32_t)(n0 + 16 * (2 * w + i) + nr) * (uint32_t)a.K + 16u * nc;
+                    gb[i] = (uint32_t)(n0 + 16 * (2 * w + i) + nr) * (uint32_t)a.K + k0 + 16u * nc;
             }
-            so = 4u * (uint32_t)(n0 + 64 * q + (lane & 31));
+            so = 4u * ((k0 / LTX_GROUP) * (uint32_t)a.N + (uint32_t)(n0 + 64 * q + (lane & 31)));
 #pragma unroll
             for (int i = 0; i < NI; i++)
 #pragma unroll
@@ -405,7 +412,11 @@ struct Q8Gemm {
             // Every wave has passed its last barrier: no stage is read or DMA'd
             // any more, and each wave stages its epilogue in a private 9 KB patch.
             uint8_t* patch = w < 3 ? q8_sa0 + 9216 * w : w < 6 ? q8_sa1 + 9216 * (w - 3) : q8_sa2 + 9216 * (w - 6);
-            gemm_epilogue_lds<T, EPI, NI, NJ>(a, acc, (float*)patch, m0 + 128 * g, n0 + 64 * q, n0);
+            if (ks_n > 1)  // a slice's partial sums; ltx_gemm_reduce_* applies the epilogue
+                gemm_store_partial<NI, NJ>(acc, (float*)patch, a.part + (size_t)ks * a.M * a.N, a.M, a.N,
+                                           m0 + 128 * g, n0 + 64 * q);
+            else
+                gemm_epilogue_lds<T, EPI, NI, NJ>(a, acc, (float*)patch, m0 + 128 * g, n0 + 64 * q, n0);
             // every patch has been read back before the next tile's DMA fills
             // the stages it lives in
             __builtin_amdgcn_sched_barrier(0);

@@ -28,10 +28,20 @@ struct Carve {
 
 struct Ws16 {
     void *n_msa, *qk16, *vt1, *qh1, *kh1, *glog1, *o1, *x_sa, *attn_in, *q2_16, *glog2, *enc, *k2_16, *vt2, *qh2,
-        *kh2, *o2, *x_ca, *ff_in, *h;
+        *kh2, *o2, *x_ca, *ff_in, *h, *part;
 };
 
-static void carve16(Carve& c, Ws16& w, size_t T, size_t S) {
+// Split-K slices of an LDS-DMA GEMM whose output tiles would fill at most
+// half the CUs: the largest power of two S <= 8 with tiles * S <= CUs and
+// K / S a multiple of 128 of at least 512 (eight K-tiles per slice).
+static int gemm_ksplit(int num_cu, int M, int N, int K) {
+    const int tiles = ((M + 255) / 256) * (N / 256);
+    int s = 1;
+    while (s < 8 && tiles * s * 2 <= num_cu && K % (256 * s) == 0 && K / (s * 2) >= 512) s *= 2;
+    return s;
+}
+
+static void carve16(Carve& c, Ws16& w, size_t T, size_t S, int num_cu) {
     const size_t D = LTX_D;
     w.n_msa = c.take(T * D * 2);
     w.qk16 = c.take(T * 2 * D * 2);
@@ -53,6 +63,16 @@ static void carve16(Carve& c, Ws16& w, size_t T, size_t S) {
     w.x_ca = c.take(T * D * 4);
     w.ff_in = c.take(T * D * 2);
     w.h = c.take(T * LTX_FF * 2);
+    // f32 partial sums of the split-K GEMMs: the largest slices * M * N over
+    // the block's seven projections (none at large T)
+    size_t part = 0;
+    const int shapes[6][3] = {{(int)T, 3 * LTX_D, LTX_D}, {(int)T, LTX_D, LTX_D}, {(int)S, 2 * LTX_D, LTX_D},
+                              {(int)T, LTX_FF, LTX_D}, {(int)T, LTX_D, LTX_FF}, {(int)T, LTX_D, LTX_D}};
+    for (const auto& sh : shapes) {
+        const int k = gemm_ksplit(num_cu, sh[0], sh[1], sh[2]);
+        if (k > 1) part = std::max(part, (size_t)k * sh[0] * sh[1] * 4);
+    }
+    w.part = part ? c.take(part) : nullptr;
 }
 
 struct Ws32 {
@@ -87,7 +107,7 @@ static void ensure_ws(ltx_ctx* c, size_t T, size_t S, int mode) {
         carve32(cv, w, T, S);
     } else {
         Ws16 w;
-        carve16(cv, w, T, S);
+        carve16(cv, w, T, S, c->num_cu);
     }
     if (c->ws.bytes < cv.off) {
         HIPC(hipDeviceSynchronize());
@@ -152,11 +172,18 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
         al16(g.out) && al16(g.out2) && al16(g.resid) && al16(g.bias) && al16(g.ada.tstab) && al16(g.ada.sst)) {
         // (its epilogue moves 16-byte vectors: outputs, residual and bias 16-byte aligned)
         g.scales = p.s2.p;
+        const char* es = epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv";
         std::snprintf(name, sizeof(name), "ltx_gemm_q8_%s%s%s", mode == LTX_MODE_BF16 ? "bf16_" : "",
-                      p.scale_f16 ? "" : "s32_",
-                      epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv");
-        const int ntiles = g.tiles_m * g.tiles_n;
-        c->launch(name, c->gemm_persistent ? std::min(ntiles, c->num_cu) : ntiles, 1, 1, 512, &g, st, label);
+                      p.scale_f16 ? "" : "s32_", es);
+        // few output tiles: split K over more workgroups (when the caller
+        // gave a buffer for the partial sums), then reduce + epilogue
+        g.ksplit = g.part ? gemm_ksplit(c->num_cu, M, p.N, p.K) : 1;
+        const int nitems = g.tiles_m * g.tiles_n * g.ksplit;
+        c->launch(name, c->gemm_persistent ? std::min(nitems, c->num_cu) : nitems, 1, 1, 512, &g, st, label);
+        if (g.ksplit > 1) {
+            std::snprintf(name, sizeof(name), "ltx_gemm_reduce_%s_%s", msuffix(mode), es);
+            c->launch(name, p.N / 64, (M + 63) / 64, 1, 256, &g, st, "splitk_reduce");
+        }
         return;
     }
     std::snprintf(name, sizeof(name), "ltx_gemm_%s_%s_%s", msuffix(mode), bk,
@@ -329,7 +356,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
                     std::to_string(w->f16_max) + " > 65504); run LTX_MODE_BF16");
     unsigned long long* sat = sat_of(c, mode);
     Ws16 b;
-    carve16(cv, b, T, S);
+    carve16(cv, b, T, S, c->num_cu);
     // self-attention: n = modulate(rms(x), ada1, ada0); fused q|k|v GEMM
     norm_mod(c, mode, x, b.n_msa, ada, T, 0, 1, st);
     LtxGemmArgs g{};
@@ -337,6 +364,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.out2 = b.vt1;
     g.nsplit = 2 * LTX_D;
     g.sat = sat;
+    g.part = (float*)b.part;  // split-K partial sums (small grids)
     gemm16(c, mode, w->qkv1, b.n_msa, T, LTX_D, LTX_EPI_QKV, g, st, "gemm:qkv1");
     // The self-attention gate logits on the side stream, beside the q/k
     // norms (both read only what the GEMMs above wrote). Side work starts
@@ -359,6 +387,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.ada = ada;
     g.igate = 2;
     g.ldo = LTX_D;
+    g.part = (float*)b.part;  // split-K partial sums (small grids)
     gemm16(c, mode, w->o1, b.o1, T, LTX_D, LTX_EPI_RESID_GATE, g, st, "gemm:o1");
     // cross-attention
     norm_mod(c, mode, (const float*)b.x_sa, b.attn_in, ada, T, 6, 7, st);
@@ -366,6 +395,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.out = b.q2_16;
     g.ldo = LTX_D;
     g.sat = sat;
+    g.part = (float*)b.part;  // split-K partial sums (small grids)
     gemm16(c, mode, w->q2, b.attn_in, T, LTX_D, LTX_EPI_STORE, g, st, "gemm:q2");
     // the cross-attention gate logits on the side stream, beside the context
     // side (K/V modulation, k|v GEMM) and the q and k norms
@@ -378,6 +408,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.out2 = b.vt2;
     g.nsplit = LTX_D;
     g.sat = sat;
+    g.part = (float*)b.part;  // split-K partial sums (small grids)
     gemm16(c, mode, w->kv2, b.enc, S, LTX_D, LTX_EPI_QKV, g, st, "gemm:kv2");
     qknorm16(c, mode, b.q2_16, LTX_D, w->qn2.p, nullptr, nullptr, b.qh2, T, kAttnC, st);
     qknorm16(c, mode, b.k2_16, LTX_D, w->kn2.p, nullptr, nullptr, b.kh2, S, 1.0f, st);
@@ -389,6 +420,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.ada = ada;
     g.igate = 8;
     g.ldo = LTX_D;
+    g.part = (float*)b.part;  // split-K partial sums (small grids)
     gemm16(c, mode, w->o2, b.o2, T, LTX_D, LTX_EPI_RESID_GATE, g, st, "gemm:o2");
     // feed-forward
     norm_mod(c, mode, (const float*)b.x_ca, b.ff_in, ada, T, 3, 4, st);
@@ -397,6 +429,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.ldo = LTX_FF;
     g.gelu = 1;
     g.sat = sat;
+    g.part = (float*)b.part;  // split-K partial sums (small grids)
     gemm16(c, mode, w->f1, b.ff_in, T, LTX_D, LTX_EPI_STORE, g, st, "gemm:ff1");
     g = LtxGemmArgs{};
     g.out = y;
@@ -404,6 +437,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.ada = ada;
     g.igate = 5;
     g.ldo = LTX_D;
+    g.part = (float*)b.part;  // split-K partial sums (small grids)
     gemm16(c, mode, w->f2, b.h, T, LTX_FF, LTX_EPI_RESID_GATE, g, st, "gemm:ff2");
 
     set_stage(c, LTX_ST_NORM_MSA, b.n_msa, TD * 2);

@@ -216,3 +216,106 @@ __device__ void gate_body(const LtxGateArgs& a) {
 
 extern "C" __global__ void __launch_bounds__(256) ltx_gate_f16(const LtxGateArgs a) { gate_body<_Float16>(a); }
 extern "C" __global__ void __launch_bounds__(256) ltx_gate_bf16(const LtxGateArgs a) { gate_body<__bf16>(a); }
+
+// Split-K completion: v = sum over s = 0 .. S-1 of part[s][m][n] (in that
+// order) + bias[n], then the GEMM's epilogue. A workgroup of 256 threads owns
+// a 64 x 64 block: thread t row t / 4, columns 16 (t % 4) .. + 15 (four
+// threads read a row's 256 contiguous bytes). V^T blocks of the QKV split
+// are transposed through LDS so that their rows (64 tokens) store whole.
+template <typename T, int EPI>
+__device__ void reduce_body(const LtxGemmArgs& a) {
+    __shared__ uint16_t tr[64][64 + 8];
+    const int t = threadIdx.x, r = t >> 2, cq = 16 * (t & 3);
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const int m = m0 + r, n = n0 + cq;
+    const bool row_ok = m < a.M;
+    const size_t MN = (size_t)a.M * a.N;
+    float v[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) v[e] = 0.0f;
+    if (row_ok) {
+        for (int s = 0; s < a.ksplit; s++) {
+            const float* p = a.part + s * MN + (size_t)m * a.N + n;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const f32x4 x = *(const f32x4*)(p + 4 * c);
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[4 * c + e] += x[e];
+            }
+        }
+        if (a.bias) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const f32x4 b = *(const f32x4*)(a.bias + n + 4 * c);
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[4 * c + e] += b[e];
+            }
+        }
+    }
+    unsigned bad = 0;  // 16-bit stores out of range (range guard)
+    if (EPI == LTX_EPI_RESID_GATE) {
+        if (row_ok) {
+            const float* gt = a.ada.tstab + ((size_t)ada_row(a.ada, m) * 9 + a.igate) * LTX_D + n;
+            const float* gs = a.ada.sst + (size_t)a.igate * LTX_D + n;
+            const float* rs = a.resid + (size_t)m * a.ldo + n;
+            float* o = (float*)a.out + (size_t)m * a.ldo + n;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const f32x4 x = *(const f32x4*)(rs + 4 * c), g0 = *(const f32x4*)(gt + 4 * c),
+                            g1 = *(const f32x4*)(gs + 4 * c);
+                f32x4 y;
+#pragma unroll
+                for (int e = 0; e < 4; e++) y[e] = x[e] + v[4 * c + e] * (g0[e] + g1[e]);
+                *(f32x4*)(o + 4 * c) = y;
+            }
+        }
+    } else if (EPI == LTX_EPI_QKV && n0 >= a.nsplit) {
+        // V^T [c][m], c = n - nsplit: through LDS, then 64-token rows
+#pragma unroll
+        for (int e = 0; e < 16; e++) tr[cq + e][r] = Op<T>::bits(v[e]);
+        if (row_ok)
+#pragma unroll
+            for (int e = 0; e < 16; e++) bad += out_of_range<T>(v[e]);
+        __syncthreads();
+        const int c = n0 - a.nsplit + r, mm = m0 + cq;  // row r of the transposed block, tokens cq ..
+        uint16_t* dst = (uint16_t*)a.out2 + (size_t)c * a.M + mm;
+        if (mm + 16 <= a.M && (a.M & 7) == 0) {
+            const u32x4* src = (const u32x4*)&tr[r][cq];
+            *(u32x4*)dst = src[0];
+            *(u32x4*)(dst + 8) = src[1];
+        } else {
+            for (int e = 0; e < 16; e++)
+                if (mm + e < a.M) dst[e] = tr[r][cq + e];
+        }
+    } else if (row_ok) {  // STORE, or the q | k rows of the QKV split
+        const bool gelu = EPI == LTX_EPI_STORE && a.gelu;
+        if (gelu)
+#pragma unroll
+            for (int e = 0; e < 16; e++) v[e] = gelu_tanh(v[e]);
+        if (EPI == LTX_EPI_STORE && a.out_f32) {
+            float* o = (float*)a.out + (size_t)m * a.ldo + n;
+#pragma unroll
+            for (int c = 0; c < 4; c++) *(f32x4*)(o + 4 * c) = f32x4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
+        } else {
+            const int ld = EPI == LTX_EPI_QKV ? a.nsplit : a.ldo;
+            uint16_t* o = (uint16_t*)a.out + (size_t)m * ld + n;
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+                *(u32x4*)(o + 8 * c) = u32x4{pack2<T>(v[8 * c], v[8 * c + 1]), pack2<T>(v[8 * c + 2], v[8 * c + 3]),
+                                             pack2<T>(v[8 * c + 4], v[8 * c + 5]), pack2<T>(v[8 * c + 6], v[8 * c + 7])};
+#pragma unroll
+            for (int e = 0; e < 16; e++) bad += out_of_range<T>(v[e]);
+        }
+    }
+    range_report(a.sat, bad);
+}
+
+#define REDUCE_KERNEL(NAME, T, EPI_) \
+    extern "C" __global__ void __launch_bounds__(256) NAME(const LtxGemmArgs a) { reduce_body<T, EPI_>(a); }
+
+REDUCE_KERNEL(ltx_gemm_reduce_f16_store, _Float16, LTX_EPI_STORE)
+REDUCE_KERNEL(ltx_gemm_reduce_f16_resid, _Float16, LTX_EPI_RESID_GATE)
+REDUCE_KERNEL(ltx_gemm_reduce_f16_qkv, _Float16, LTX_EPI_QKV)
+REDUCE_KERNEL(ltx_gemm_reduce_bf16_store, __bf16, LTX_EPI_STORE)
+REDUCE_KERNEL(ltx_gemm_reduce_bf16_resid, __bf16, LTX_EPI_RESID_GATE)
+REDUCE_KERNEL(ltx_gemm_reduce_bf16_qkv, __bf16, LTX_EPI_QKV)

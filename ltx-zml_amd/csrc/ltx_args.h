@@ -85,6 +85,8 @@ typedef struct {
     uint32_t qxor;        // int8 kinds: XOR taking each weight byte to q + 128 (0x80808080 for plain int8,
                           // 0 for bytes stored as q + 128); the LDS-DMA kernels take the latter only
     unsigned long long* sat;  // range guard counter of the 16-bit outputs (V^T, 16-bit stores) or NULL
+    int ksplit;           // split-K (LDS-DMA kernel): 1, or S slices of K / S each, whose f32 partial sums
+    float* part;          // go to part [S][M][N] for ltx_gemm_reduce_* to finish with the epilogue
 } LtxGemmArgs;
 
 // Full-row qk RMSNorm (weighted, over all 4096 channels) + optional split-half
