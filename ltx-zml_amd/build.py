@@ -6,6 +6,8 @@
 3. Host runtime (csrc/host/*.cpp, plain C++ over the HIP runtime API; and
    csrc/host/*.hip, host code with a device array of its own, by hipcc) + the
    embedded objects -> libltx_amd.so next to this file.
+4. csrc/tools/mfma_ceiling.hip -> mfma_ceiling next to this file (the
+   practical MFMA-rate ceiling that the benchmark's roofline is read against).
 
 Usage: python ltx-zml_amd/build.py [-v]
 """
@@ -22,6 +24,7 @@ PKG = pathlib.Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libltx_amd.so"
+CEILING = PKG / "mfma_ceiling"
 INCLUDE = PKG.parent / "include"
 ROCM = pathlib.Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 KERNELS = ["k_gemm", "k_attn", "k_norm", "k_f32", "k_core"]
@@ -75,6 +78,7 @@ def build(verbose: bool = False) -> pathlib.Path:
         jobs.append([hipcc, *HIP_HOST_FLAGS, f"-I{CSRC}", f"-I{INCLUDE}", "-c", str(CSRC / "host" / f"{h}.hip"),
                      "-o", str(o)])
         objs.append(o)
+    jobs.append([hipcc, *HIP_HOST_FLAGS, str(CSRC / "tools" / "mfma_ceiling.hip"), "-o", str(CEILING)])
     with cf.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
         list(ex.map(lambda c: _run(c, verbose), jobs))
     _run(["g++", "-c", str(asm), "-o", str(BUILD / "ltx_codeobjects.o")], verbose)

@@ -31,7 +31,7 @@ struct Ws16 {
         *kh2, *o2, *x_ca, *ff_in, *h, *part;
 };
 
-// Split-K slices of an LDS-DMA GEMM whose output tiles would fill at most
+// Split-K slices of a GEMM whose 256 x 256 output tiles would fill at most
 // half the CUs: the largest power of two S <= 8 with tiles * S <= CUs and
 // K / S a multiple of 128 of at least 512 (eight K-tiles per slice).
 static int gemm_ksplit(int num_cu, int M, int N, int K) {
@@ -186,14 +186,29 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
         }
         return;
     }
-    std::snprintf(name, sizeof(name), "ltx_gemm_%s_%s_%s", msuffix(mode), bk,
-                  epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv");
-    c->launch(name, g.tiles_m * g.tiles_n, 1, 1, 512, &g, st, label);
+    const char* es = epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv";
+    std::snprintf(name, sizeof(name), "ltx_gemm_%s_%s_%s", msuffix(mode), bk, es);
+    // split-K as above; the reduce kernel moves 16-byte vectors, so only with
+    // aligned operands
+    const bool aligned = g.ldo % 8 == 0 && al16(g.out) && al16(g.out2) && al16(g.resid) && al16(g.bias) &&
+                         al16(g.ada.tstab) && al16(g.ada.sst);
+    g.ksplit = g.part && aligned ? gemm_ksplit(c->num_cu, M, p.N, p.K) : 1;
+    c->launch(name, g.tiles_m * g.tiles_n * g.ksplit, 1, 1, 512, &g, st, label);
+    if (g.ksplit > 1) {
+        std::snprintf(name, sizeof(name), "ltx_gemm_reduce_%s_%s", msuffix(mode), es);
+        c->launch(name, p.N / 64, (M + 63) / 64, 1, 256, &g, st, "splitk_reduce");
+    }
 }
 
 static void gate16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M, float* out, hipStream_t st) {
     LtxGateArgs g{A, mode == LTX_MODE_BF16 ? p.w_bf16.p : p.w_f16.p, (const float*)p.bias.p, out, M};
-    c->launch(mode == LTX_MODE_BF16 ? "ltx_gate_bf16" : "ltx_gate_f16", (M + 127) / 128, 1, 1, 256, &g, st);
+    // one wave per 32 rows while that gives every CU at least one wave
+    // (each wave's 256 MFMAs form one dependent chain); below that, K split
+    // over the four waves of a workgroup per 32 rows
+    if ((M + 31) / 32 >= c->num_cu)
+        c->launch(mode == LTX_MODE_BF16 ? "ltx_gate_bf16" : "ltx_gate_f16", (M + 127) / 128, 1, 1, 256, &g, st);
+    else
+        c->launch(mode == LTX_MODE_BF16 ? "ltx_gate_ks_bf16" : "ltx_gate_ks_f16", (M + 31) / 32, 1, 1, 256, &g, st);
 }
 
 // The attention's exponent scale: softmax scale 1/sqrt(128) times log2(e).

@@ -97,8 +97,11 @@ __device__ void gemm_body(const LtxGemmArgs& a) {
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wm = w / WNW, wn = w % WNW;
-    TileIdx ti = tile_of(blockIdx.x, a.tiles_m, a.tiles_n);
+    // split-K: workgroup b computes slice b % ksplit of K for tile b / ksplit
+    const int ks_n = a.ksplit > 1 ? a.ksplit : 1;
+    TileIdx ti = tile_of(blockIdx.x / ks_n, a.tiles_m, a.tiles_n);
     const int m0 = ti.tm * BM, n0 = ti.tn * BN;
+    const int kc = a.K / ks_n, kb = (blockIdx.x % ks_n) * kc;  // this slice: k in [kb, kb + kc)
 
     f32x16 acc[NI][NJ];
 #pragma unroll
@@ -107,8 +110,8 @@ __device__ void gemm_body(const LtxGemmArgs& a) {
         for (int j = 0; j < NJ; j++) acc[i][j] = f32x16{0};
 
     Stage<T, BKIND, NT> st;
-    const int nk = a.K / BK;
-    st.load(a, m0, n0, 0, tid);
+    const int nk = kc / BK;
+    st.load(a, m0, n0, kb, tid);
     st.store(sA[0], sB[0], tid);
     __syncthreads();
 
@@ -131,7 +134,7 @@ __device__ void gemm_body(const LtxGemmArgs& a) {
     for (int kt = 0; kt < nk; kt++) {
         const int buf = kt & 1;
         const bool more = kt + 1 < nk;
-        if (more) st.load(a, m0, n0, (kt + 1) * BK, tid);
+        if (more) st.load(a, m0, n0, kb + (kt + 1) * BK, tid);
 #pragma unroll
         for (int kk = 0; kk < BK / 16; kk++) {
             const int cur = kk & 1;
@@ -147,6 +150,20 @@ __device__ void gemm_body(const LtxGemmArgs& a) {
     }
 
     // acc[i][j][r]: row 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4, column 32 j + lane % 32
+    if (ks_n > 1) {  // the slice's partial sums; ltx_gemm_reduce_* applies the epilogue
+        float* part = a.part + (size_t)(blockIdx.x % ks_n) * a.M * a.N;
+        const int mr = m0 + wm * 128 + 4 * (lane >> 5), nc = n0 + wn * WN + (lane & 31);
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int m = mr + 32 * i + 8 * (r >> 2) + (r & 3);
+                    if (m < a.M) part[(size_t)m * a.N + nc + 32 * j] = acc[i][j][r];
+                }
+        return;
+    }
     gemm_epilogue<T, EPI, NI, NJ>(a, acc, m0 + wm * 128 + 4 * (lane >> 5), n0 + wn * WN + (lane & 31), n0);
 }
 
@@ -216,6 +233,43 @@ __device__ void gate_body(const LtxGateArgs& a) {
 
 extern "C" __global__ void __launch_bounds__(256) ltx_gate_f16(const LtxGateArgs a) { gate_body<_Float16>(a); }
 extern "C" __global__ void __launch_bounds__(256) ltx_gate_bf16(const LtxGateArgs a) { gate_body<__bf16>(a); }
+
+// The same logits for few rows: one workgroup per 32 rows, wave q sums
+// k in [1024 q, 1024 q + 1024) over two alternating accumulators (two
+// independent MFMA chains), and wave 0 adds the four partial sums in wave
+// order through LDS.
+template <typename T>
+__device__ void gate_ks_body(const LtxGateArgs& a) {
+    typedef typename Op<T>::v8 v8;
+    __shared__ f32x16 red[3][64];
+    const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const int m0 = blockIdx.x * 32;
+    const int fr = lane & 31, fk = 8 * (lane >> 5) + q * (LTX_D / 4);
+    const uint16_t* pa = (const uint16_t*)a.a + (size_t)min(m0 + fr, a.M - 1) * LTX_D + fk;
+    const uint16_t* pb = (const uint16_t*)a.gw + (size_t)fr * LTX_D + fk;
+    f32x16 acc0 = f32x16{0}, acc1 = f32x16{0};
+#pragma unroll 8
+    for (int k = 0; k < LTX_D / 4; k += 32) {
+        acc0 = Op<T>::mfma32(__builtin_bit_cast(v8, *(const u32x4*)(pa + k)),
+                             __builtin_bit_cast(v8, *(const u32x4*)(pb + k)), acc0);
+        acc1 = Op<T>::mfma32(__builtin_bit_cast(v8, *(const u32x4*)(pa + k + 16)),
+                             __builtin_bit_cast(v8, *(const u32x4*)(pb + k + 16)), acc1);
+    }
+    const f32x16 acc = acc0 + acc1;
+    if (q > 0) red[q - 1][lane] = acc;
+    __syncthreads();
+    if (q > 0) return;
+    const f32x16 sum = ((acc + red[0][lane]) + red[1][lane]) + red[2][lane];
+    const float bias = a.gb[fr];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        int m = m0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < a.M) a.out[(size_t)m * LTX_H + fr] = sum[r] + bias;
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) ltx_gate_ks_f16(const LtxGateArgs a) { gate_ks_body<_Float16>(a); }
+extern "C" __global__ void __launch_bounds__(256) ltx_gate_ks_bf16(const LtxGateArgs a) { gate_ks_body<__bf16>(a); }
 
 // Split-K completion: v = sum over s = 0 .. S-1 of part[s][m][n] (in that
 // order) + bias[n], then the GEMM's epilogue. A workgroup of 256 threads owns
