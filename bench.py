@@ -44,6 +44,23 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def mfma_ceiling():
+    """The practical MFMA rate of this GPU, measured beside the benchmark by
+    ltx-zml_amd/mfma_ceiling (a child process): v_mfma_f32_32x32x16 loops on
+    random f16 / bf16 operands, A from registers or from one LDS read per
+    MFMA. The board's power limit holds these well below the published
+    dense peak; None when the tool is not built."""
+    exe = ROOT / "ltx-zml_amd" / "mfma_ceiling"
+    if not exe.exists():
+        return None
+    import subprocess
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    if r.returncode != 0:
+        log(f"bench: mfma_ceiling failed ({r.returncode}): {r.stderr[-300:]}")
+        return None
+    return json.loads(r.stdout.strip().splitlines()[-1])["tflops"]
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -523,6 +540,7 @@ def main() -> int:
         log(f"bench: denoise {res['denoise']['denoise_s']:.2f} s, "
             f"{res['denoise']['ms_per_block_call']:.2f} ms per block call")
     ctx.close()
+    res["mfma_ceiling_tflops"] = mfma_ceiling()
     if not args.no_cpu_baseline:
         threads = cpu_threads()
         log(f"bench: CPU baseline on {threads} threads")

@@ -98,7 +98,7 @@ struct Variant {
 };
 
 int main(int argc, char** argv) {
-    const int nwg = 1024, iters = argc > 1 ? std::max(1, atoi(argv[1])) : 100;
+    const int nwg = 1024, iters = argc > 1 ? std::max(1, atoi(argv[1])) : 500;
     float* out = nullptr;
     if (hipMalloc(&out, (size_t)nwg * 512 * sizeof(float)) != hipSuccess) {
         fprintf(stderr, "hipMalloc failed\n");
