@@ -28,10 +28,11 @@ sys.path.insert(0, str(ROOT))
 
 D, H, HD, FF = 4096, 32, 128, 16384
 PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
-# HBM bytes per self-attention launch from rocprofv3 FETCH_SIZE (x2.0, the
-# factor a 1 GiB copy calibrates) + WRITE_SIZE (x1.0), for the kernel as
-# built at that measurement (profiles/attn_self_t28672_f16_hbm_bytes.md).
-ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.474e9}
+# HBM bytes per self-attention launch, by (tokens, operand type): rocprofv3
+# FETCH_SIZE x 2.0 (the factor a 1 GiB copy calibrates) + WRITE_SIZE x 1.0,
+# measured on this kernel (profiles/block_t28672_hbm_bytes.md); None for a
+# size or type not profiled.
+ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.473e9, (28672, "bf16"): 2.470e9}
 
 
 def flops(T: int, S: int) -> dict:

@@ -9,7 +9,7 @@
 // one workgroup holds a CU; each wave runs ITERS x 16 MFMAs over four
 // accumulators, fragments read four MFMAs ahead. LDS reads stay in the first
 // 16 KB (index < 1024 of u32x4). Prints one JSON line: TFLOP/s per variant,
-// the median of 5 timed launches after one warm-up launch.
+// the median of 7 timed launches after one warm-up round.
 //
 // Build: part of ltx-zml_amd/build.py (-> ltx-zml_amd/mfma_ceiling).
 #include <hip/hip_runtime.h>
@@ -114,22 +114,23 @@ int main(int argc, char** argv) {
     const double flop = (double)nwg * 8 * iters * 16 * (32.0 * 32 * 16 * 2);
     printf("{\"tool\": \"mfma_ceiling\", \"workgroups\": %d, \"waves_per_simd\": 2, \"iters\": %d, \"tflops\": {", nwg,
            iters);
-    bool first = true;
-    for (const Variant& v : vars) {
-        std::vector<float> ms;
-        for (int rep = 0; rep < 6; rep++) {
+    // variants interleaved launch by launch, so that a drift of the clock
+    // over the run (temperature, power state) spreads over all of them
+    constexpr int NV = sizeof(vars) / sizeof(vars[0]), REPS = 7;
+    std::vector<float> ms[NV];
+    for (int rep = 0; rep <= REPS; rep++)
+        for (int i = 0; i < NV; i++) {
             hipEventRecord(e0);
-            hipLaunchKernelGGL(v.kern, dim3(nwg), dim3(512), 0, 0, out, iters);
+            hipLaunchKernelGGL(vars[i].kern, dim3(nwg), dim3(512), 0, 0, out, iters);
             hipEventRecord(e1);
             if (hipEventSynchronize(e1) != hipSuccess) return 2;
             float t = 0.0f;
             hipEventElapsedTime(&t, e0, e1);
-            if (rep) ms.push_back(t);
+            if (rep) ms[i].push_back(t);  // round 0 warms up
         }
-        std::sort(ms.begin(), ms.end());
-        printf("%s\"%s\": %.1f", first ? "" : ", ", v.name, flop / (ms[ms.size() / 2] * 1e-3) / 1e12);
-        first = false;
-        fflush(stdout);
+    for (int i = 0; i < NV; i++) {
+        std::sort(ms[i].begin(), ms[i].end());
+        printf("%s\"%s\": %.1f", i ? ", " : "", vars[i].name, flop / (ms[i][REPS / 2] * 1e-3) / 1e12);
     }
     printf("}}\n");
     if (hipGetLastError() != hipSuccess) return 2;
