@@ -9,14 +9,15 @@
 //   and V^T staged through registers into LDS, keys past lkv masked.
 //
 // Both compute the scores TRANSPOSED, S^T = K . Q^T, and the output as
-// O^T = V^T . P^T, with v_mfma_f32_32x32x16: the query is then the MFMA
-// column index, so lane l always holds query l % 32 — its running max m,
-// partial sum l and its O^T column stay lane-local, and only the tile max
-// needs one exchange with lane l ^ 32. The P^T operand comes straight from
-// the S^T accumulators (no LDS round trip): within every 16-key chunk the
-// keys are consumed in the order 0-3, 8-11, 4-7, 12-15, which is the order
-// the accumulator layout hands them to each lane, and the K (or V^T) tile is
-// stored in LDS permuted to match.
+// O^T = V^T . P^T: the query is then the MFMA column index, so a query's
+// running max m, partial sums l and O^T column stay in the few lanes that
+// hold that column, and only the tile max needs an exchange between them.
+// The P^T operand comes straight from the S^T accumulators (no LDS round
+// trip): the K tile is stored in LDS with its rows permuted so that the
+// accumulator layout hands each lane the keys of its P^T operand in order.
+// The w8 kernel uses v_mfma_f32_32x32x16 (lane l holds query l % 32; within
+// every 16-key chunk the keys are consumed in the order 0-3, 8-11, 4-7,
+// 12-15), the ping-pong kernel v_mfma_f32_16x16x32 (below).
 //
 // Statistics are f32. Softmax uses exp2 with the 1/sqrt(128) scale folded
 // into the exponent (s * C - m * C, C = scale * log2 e); m starts at -FLT_MAX
@@ -276,19 +277,43 @@ __device__ __forceinline__ float asp_xhalf_max(float x) {
 }
 
 // ---------------------------------------------------------------------------
+// max of x over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (one query's lanes
+// in the 16 x 16 layout)
+__device__ __forceinline__ float asp_quad_max(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    x = fmaxf(x, fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])));
+    return asp_xhalf_max(x);
+}
+
+// ---------------------------------------------------------------------------
 // Ping-pong kernel for whole 64-key tiles (lkv % 64 == 0, at least two
-// tiles): 8 waves of 32 queries; waves w and w + 4 share a SIMD and run one
-// phase apart. A wave alternates an MFMA phase (PV(t-1) then S(t), fragments
-// from LDS) with a softmax phase (softmax(t), the rare output rescale, and
-// the DMA of K(t+2) and V(t+1)), so at any time one wave of each SIMD feeds
-// the matrix core while the other runs the VALU work. One s_barrier per
-// phase keeps the pairing.
+// tiles), on v_mfma_f32_16x16x32: 8 waves of 32 queries; waves w and w + 4
+// share a SIMD and run one phase apart. A wave alternates an MFMA phase
+// (PV(t-1) then S(t), fragments from LDS) with a softmax phase (softmax(t),
+// the rare output rescale, and the DMA of K(t+2) and V(t+1)), so at any time
+// one wave of each SIMD feeds the matrix core while the other runs the VALU
+// work. One s_barrier per phase keeps the pairing. At equal flops the
+// 16 x 16 x 32 MFMA runs faster than 32 x 32 x 16 at the board's
+// power-limited clock (self-attention at 28,672 tokens: 10.15 against
+// 10.88 ms on one box), with the same LDS bytes per flop: every 1 KB K or
+// V^T fragment feeds the MFMAs of both query blocks.
 //
-// LDS: K tiles of 64 rows x 256 B with rows permuted within each group of 16
-// keys (as in the pipelined kernel: the S^T accumulators then hand the PV
-// MFMA 8 consecutive keys per 16-key step) and 16-byte chunk c of row r in
-// slot c ^ (r & 15); V^T tiles of 128 rows x 128 B with chunk c of row d in
-// slot c ^ ((d >> 1) & 7). Three stages each, distinct objects.
+// Layout (16 x 16 x 32: A lane l = row l % 16, k 8 (l / 16) .. + 7; B lane l
+// = column l % 16, same k; D lane l = column l % 16, rows 4 (l / 16) .. + 3):
+// - a wave's 32 queries are two column blocks qb; lane l holds queries
+//   16 qb + l % 16, so each query's scores live in the four lanes l % 16 +
+//   16 j, which share its running max (one exchange over l ^ 16, l ^ 32);
+// - S^T = K . Q^T in four 16-key blocks kb, four 32-dim steps;
+// - O^T = V^T . P^T in eight 16-dim blocks db, two 32-key steps kc. The P^T
+//   operand of step kc is the lane's own accumulators of key blocks 2 kc and
+//   2 kc + 1 (4 + 4 values): LDS row R of a K tile holds key
+//   32 R5 + 16 R3 + 8 R2 + 4 R4 + 2 R1 + R0 (bits of R), so that these
+//   8 values are keys 8 (l / 16) .. + 7 of the step, in V^T's natural order.
+//
+// LDS: K tiles of 64 rows x 256 B, 16-byte chunk c of row r in slot
+// c ^ (r & 15); V^T tiles of 128 rows x 128 B with chunk c of row d in slot
+// c ^ ((d >> 1) & 7). Three stages each, distinct objects.
 //
 // DMA and waits (G0 = waves 0-3 lead, G1 = waves 4-7 follow one phase
 // later): G0 issues all of K(t+2) and V(t+1) (its slices and G1's) at the
@@ -299,6 +324,10 @@ __device__ __forceinline__ float asp_xhalf_max(float x) {
 // them. G1 issues no DMA: its softmax phase runs one phase after G0's, so
 // slices it issued would have only one phase to land (measured 1 % slower
 // on the whole kernel).
+//
+// The softmax state (running max m, partial sums l) is held in vector
+// values: as arrays in the kernel's state the compiler placed them in LDS,
+// which added LDS round trips and waits to every phase (10 % slower).
 __shared__ __attribute__((aligned(1024))) uint8_t app_k0[16384];
 __shared__ __attribute__((aligned(1024))) uint8_t app_k1[16384];
 __shared__ __attribute__((aligned(1024))) uint8_t app_k2[16384];
@@ -315,6 +344,7 @@ __device__ __forceinline__ uint8_t* app_v() {
     return S == 0 ? app_v0 : S == 1 ? app_v1 : app_v2;
 }
 
+
 // PS: Q arrives multiplied by the exponent scale C = log2(e)/sqrt(128) (the
 // block's qk-norm kernel writes it so), so a score is already in exp2 units.
 template <typename T, bool PS>
@@ -324,23 +354,22 @@ struct AttnPP {
     __amdgpu_buffer_rsrc_t rk, rv;
     uint32_t gk[2], gv[2];  // per-lane DMA source offsets in tile 0
     int lw;                 // this wave's 2 KB slice of a stage
-    uint32_t ok[8];         // K fragment offsets per 16-dim step c (kb adds 8192)
-    uint32_t ov[4];         // V^T fragment offsets per 16-key step kc (db adds 4096)
-    v8 qf[8];
-    f32x16 o[4];
-    f32x16 s[2];
-    v8 pf[4];
-    f32x16 sb;  // -m in every element: the S MFMAs start from it, so s holds s - m
-    float m, l, C;
+    uint32_t ok[4];         // K fragment offsets per 32-dim step ks (kb adds 4096)
+    uint32_t ov[2];         // V^T fragment offsets per 32-key step kc (db adds 2048)
+    v8 qf[2][4];            // Q^T operand [qb][ks]
+    f32x4 o[8][2];          // O^T [db][qb]
+    f32x4 s[4][2];          // S^T [kb][qb]
+    v8 pf[2][2];            // P^T operand [kc][qb]
+    f32x4 sb[2];            // -m of the lane's query in block qb: the S MFMAs start from it
+    f32x2 m, l;             // running max and partial sum per query block (vectors, not arrays: kept in registers)
+    float C;
     int nt, g;
 
     __device__ __forceinline__ AttnPP(const LtxAttnArgs& args) : a(args) {}
 
     // Group 0 (waves 0-3) issues every DMA: wave w fills its own 2 KB slice
     // of a stage and that of wave w + 4 (8 KB further, K rows + 32 = keys
-    // + 32, V^T rows + 64), 4 instructions per K or V tile. Group 0 issues in
-    // its softmax phase t, two phases before its MFMA phase t + 2 needs the
-    // tile (group 1's slices, issued in its own softmax phase, had only one).
+    // + 32, V^T rows + 64), 4 instructions per K or V tile.
     template <int S>
     __device__ __forceinline__ void dma_k(int t) {
         uint8_t* d = app_k<S>() + lw;
@@ -362,89 +391,106 @@ struct AttnPP {
                                                          t * 128 + 128 * a.lkv * h, 0, 0);
     }
 
-    // MFMA phase t: PV(t-1) from V stage VS, then S(t) from K stage KS
+    // MFMA phase t: PV(t-1) from V stage VS, then S(t) from K stage KS; each
+    // fragment feeds the MFMAs of both query blocks
     template <int KS, int VS>
     __device__ __forceinline__ void mfma_phase(bool ds, bool dp) {
         if (dp) {
             const uint8_t* sv = app_v<VS>();
 #pragma unroll
-            for (int kc = 0; kc < 4; kc++)
+            for (int kc = 0; kc < 2; kc++)
 #pragma unroll
-                for (int db = 0; db < 4; db++) {
-                    const v8 vf = __builtin_bit_cast(v8, *(const u32x4*)(sv + ov[kc] + 4096 * db));
-                    o[db] = Op<T>::mfma32(vf, pf[kc], o[db]);
+                for (int db = 0; db < 8; db++) {
+                    const v8 vf = __builtin_bit_cast(v8, *(const u32x4*)(sv + ov[kc] + 2048 * db));
+                    o[db][0] = Op<T>::mfma16(vf, pf[kc][0], o[db][0]);
+                    o[db][1] = Op<T>::mfma16(vf, pf[kc][1], o[db][1]);
                 }
         }
         if (ds) {
             const uint8_t* sk = app_k<KS>();
-            s[0] = sb;
-            s[1] = sb;
 #pragma unroll
-            for (int c = 0; c < 8; c++)
+            for (int kb = 0; kb < 4; kb++) {
+                s[kb][0] = sb[0];
+                s[kb][1] = sb[1];
+            }
 #pragma unroll
-                for (int kb = 0; kb < 2; kb++) {
-                    const v8 kf = __builtin_bit_cast(v8, *(const u32x4*)(sk + ok[c] + 8192 * kb));
-                    s[kb] = Op<T>::mfma32(kf, qf[c], s[kb]);
+            for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++) {
+                    const v8 kf = __builtin_bit_cast(v8, *(const u32x4*)(sk + ok[ks] + 4096 * kb));
+                    s[kb][0] = Op<T>::mfma16(kf, qf[0][ks], s[kb][0]);
+                    s[kb][1] = Op<T>::mfma16(kf, qf[1][ks], s[kb][1]);
                 }
         }
-        // fragment reads four MFMAs ahead (masks: 0x100 DS read, 0x008 MFMA)
+        // fragment reads eight MFMAs (four reads) ahead (masks: 0x100 DS
+        // read, 0x008 MFMA)
         __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
         for (int i = 0; i < 32; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
             if (i < 28) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
     }
 
-    // P^T operands and their row sum. s holds score - m (the MFMAs start from
-    // sb = -m), so the weight is exp2(s) with Q pre-scaled (PS), else
-    // exp2(s C); ADJ subtracts a further max shift delta. The row sum adds
-    // exactly the rounded 16-bit weights that feed the MFMA, on the VALU.
+    // P^T operands and their row sums, per query block. s holds score - m
+    // (the MFMAs start from sb = -m), so the weight is exp2(s) with Q
+    // pre-scaled (PS), else exp2(s C); ADJ subtracts a further max shift
+    // delta. The row sum adds exactly the rounded 16-bit weights that feed
+    // the MFMA, on the VALU.
     template <bool ADJ>
-    __device__ __forceinline__ float exps(float delta) {
-        float ps = 0.f;
+    __device__ __forceinline__ f32x2 exps(f32x2 delta) {
+        f32x2 ps = {0.f, 0.f};
 #pragma unroll
-        for (int kc = 0; kc < 4; kc++) {
-            float p[8];
+        for (int kc = 0; kc < 2; kc++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                float x = s[kc >> 1][8 * (kc & 1) + e];
-                if (ADJ) x -= delta;
-                p[e] = __builtin_amdgcn_exp2f(PS ? x : x * C);
+            for (int qb = 0; qb < 2; qb++) {
+                float p[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    float x = s[2 * kc + (e >> 2)][qb][e & 3];
+                    if (ADJ) x -= delta[qb];
+                    p[e] = __builtin_amdgcn_exp2f(PS ? x : x * C);
+                }
+                const uint32_t w0 = Op<T>::cvt2(p[0], p[1]), w1 = Op<T>::cvt2(p[2], p[3]),
+                               w2 = Op<T>::cvt2(p[4], p[5]), w3 = Op<T>::cvt2(p[6], p[7]);
+                float t = ps[qb];
+                t = Op<T>::sum2(w0, t);
+                t = Op<T>::sum2(w1, t);
+                t = Op<T>::sum2(w2, t);
+                t = Op<T>::sum2(w3, t);
+                ps[qb] = t;
+                pf[kc][qb] = __builtin_bit_cast(v8, (u32x4){w0, w1, w2, w3});
             }
-            const uint32_t w0 = Op<T>::cvt2(p[0], p[1]), w1 = Op<T>::cvt2(p[2], p[3]),
-                           w2 = Op<T>::cvt2(p[4], p[5]), w3 = Op<T>::cvt2(p[6], p[7]);
-            ps = Op<T>::sum2(w0, ps);
-            ps = Op<T>::sum2(w1, ps);
-            ps = Op<T>::sum2(w2, ps);
-            ps = Op<T>::sum2(w3, ps);
-            pf[kc] = __builtin_bit_cast(v8, (u32x4){w0, w1, w2, w3});
-        }
         return ps;
     }
 
     // softmax phase: S^T accumulators -> P^T operands. The weights are first
     // formed with the running max; only if some lane's sum of its rounded
     // weights exceeds 2^8 (a weight above 2^8, or an f16 overflow, which sums
-    // to inf) is the tile max taken, the max moved, the output and row sum
-    // rescaled (after PV(t-1), before PV(t)) and the weights formed again.
-    // The first tile always takes that path and sets m to its max.
+    // to inf) is the tile max taken (over the query's four lanes), the max
+    // moved, the output and row sum rescaled (after PV(t-1), before PV(t))
+    // and the weights formed again. The first tile always takes that path
+    // and sets m to its max.
     __device__ __forceinline__ void softmax(bool first) {
-        float ps = exps<false>(0.f);
-        if (first || __builtin_amdgcn_ballot_w64(!(ps <= 256.0f)) != 0) {
-            float mx = s[0][0];
+        f32x2 ps = exps<false>(f32x2{0.f, 0.f});
+        if (first || __builtin_amdgcn_ballot_w64(!(ps[0] <= 256.0f) || !(ps[1] <= 256.0f)) != 0) {
+            f32x2 delta;
 #pragma unroll
-            for (int r = 1; r < 16; r++) mx = fmaxf(mx, s[0][r]);
+            for (int qb = 0; qb < 2; qb++) {
+                float mx = s[0][qb][0];
 #pragma unroll
-            for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[1][r]);
-            mx = asp_xhalf_max(mx);  // tile max relative to m
-            const float delta = first ? mx : fmaxf(mx, 0.f);
-            const float corr = first ? 0.f : __builtin_amdgcn_exp2f(PS ? -delta : -delta * C);
-            m += delta;
-            l *= corr;
+                for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-            for (int db = 0; db < 4; db++) o[db] *= corr;
-            sb = f32x16{0} - m;
+                    for (int r = 0; r < 4; r++) mx = fmaxf(mx, s[kb][qb][r]);
+                mx = asp_quad_max(mx);  // tile max relative to m
+                delta[qb] = first ? mx : fmaxf(mx, 0.f);
+                const float corr = first ? 0.f : __builtin_amdgcn_exp2f(PS ? -delta[qb] : -delta[qb] * C);
+                m[qb] += delta[qb];
+                l[qb] *= corr;
+#pragma unroll
+                for (int db = 0; db < 8; db++) o[db][qb] *= corr;
+                sb[qb] = f32x4{0} - m[qb];
+            }
             ps = exps<true>(delta);
         }
         l += ps;
@@ -459,11 +505,10 @@ struct AttnPP {
 
     // MFMA phase t then softmax phase t (T3 = t mod 3); returns after the
     // softmax phase's barrier (or after the MFMA phase's when t == nt).
-    // FULL: 1 <= t and t + 2 < nt, every operation present.
+    // FULL: 1 <= t and t + 2 < nt, every operation present. The wave in its
+    // MFMA phase takes issue priority over the other wave of its SIMD.
     template <int T3, bool FULL>
     __device__ __forceinline__ void step(int t) {
-        // the wave in its MFMA phase takes issue priority over the other wave
-        // of its SIMD (without it the lower-numbered waves win either way)
         __builtin_amdgcn_s_setprio(1);
         mfma_phase<T3, (T3 + 2) % 3>(FULL || t < nt, FULL || t >= 1);
         __builtin_amdgcn_sched_barrier(0);
@@ -477,15 +522,13 @@ struct AttnPP {
         }
         __builtin_amdgcn_sched_barrier(0);
         softmax(!FULL && t == 0);
-        // the P^T operands, row sum and bias must exist before the phase ends
-        // (no pass may sink them into the next MFMA phase)
 #pragma unroll
-        for (int kc = 0; kc < 4; kc++) asm volatile("" ::"v"(__builtin_bit_cast(u32x4, pf[kc])));
+        for (int kc = 0; kc < 2; kc++)
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) asm volatile("" ::"v"(__builtin_bit_cast(u32x4, pf[kc][qb])));
         asm volatile("" ::"v"(l), "v"(m));
-        asm volatile("" ::"v"(sb));
+        asm volatile("" ::"v"(sb[0]), "v"(sb[1]));
         __builtin_amdgcn_sched_barrier(0);
-        // group 0: the previous phase's tiles have landed (this phase's may
-        // still be in flight)
         if (g == 0) {
             if (dk && dv)
                 __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(8));
@@ -516,11 +559,12 @@ struct AttnPP {
                                                lkv * LTX_HD * 2, ASP_RSRC_W3);
         lw = 2048 * w;
         // DMA sources: K instruction i of wave w fills LDS rows 4 (2 w + i) ..
-        // +3 (16 lanes a row); V^T rows 8 (2 w + i) .. +7 (8 lanes a row)
+        // +3 (16 lanes a row; row R holds key perm(R), the +32 half likewise);
+        // V^T rows 8 (2 w + i) .. +7 (8 lanes a row)
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const int r = 4 * (2 * w + i) + (lane >> 4);  // LDS row = key slot
-            const int key = (r & ~15) | (r & 3) | ((r & 4) << 1) | ((r & 8) >> 1);
+            const int r = 4 * (2 * w + i) + (lane >> 4);  // LDS row within the first 32
+            const int key = (r & 3) | ((r & 16) >> 2) | ((r & 4) << 1) | ((r & 8) << 1);
             const int c = (lane & 15) ^ (r & 15);
             gk[i] = (uint32_t)key * 256u + 16u * c;
             const int d = 8 * (2 * w + i) + (lane >> 3);
@@ -528,22 +572,24 @@ struct AttnPP {
             gv[i] = (uint32_t)d * (uint32_t)lkv * 2u + 16u * cv;
         }
         {
-            const int hh = lane >> 5, r = lane & 31;
+            const int j = lane >> 4, r = lane & 15;
 #pragma unroll
-            for (int c = 0; c < 8; c++) ok[c] = r * 256 + 16 * ((2 * c + hh) ^ (r & 15));
+            for (int ks = 0; ks < 4; ks++) ok[ks] = r * 256 + 16 * ((4 * ks + j) ^ r);
 #pragma unroll
-            for (int kc = 0; kc < 4; kc++) ov[kc] = r * 128 + 16 * ((2 * kc + hh) ^ ((r >> 1) & 7));
-            const int q = min(q0 + r, lq - 1);
+            for (int kc = 0; kc < 2; kc++) ov[kc] = r * 128 + 16 * ((4 * kc + j) ^ (r >> 1));
 #pragma unroll
-            for (int c = 0; c < 8; c++)
-                qf[c] = __builtin_bit_cast(v8, *(const u32x4*)(Q + (size_t)q * LTX_HD + 16 * c + 8 * hh));
+            for (int qb = 0; qb < 2; qb++) {
+                const int q = min(q0 + 16 * qb + r, lq - 1);
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++)
+                    qf[qb][ks] = __builtin_bit_cast(v8, *(const u32x4*)(Q + (size_t)q * LTX_HD + 32 * ks + 8 * j));
+            }
         }
 #pragma unroll
-        for (int db = 0; db < 4; db++) o[db] = f32x16{0};
-        m = 0.f;
-        sb = f32x16{0};
-        l = 0.f;
-        // prologue (group 0): K(0), K(1), V(0); MFMA phase 0 needs K(0)
+        for (int db = 0; db < 8; db++) o[db][0] = o[db][1] = f32x4{0};
+        m = f32x2{0.f, 0.f};
+        sb[0] = sb[1] = f32x4{0};
+        l = f32x2{0.f, 0.f};
         if (g == 0) {
             dma_k<0>(0);
             dma_k<1>(1);
@@ -551,9 +597,7 @@ struct AttnPP {
             __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(8));
         }
         __builtin_amdgcn_s_barrier();
-        if (g == 1) __builtin_amdgcn_s_barrier();  // the second wave of each SIMD starts one phase later
-        // steps 0 .. nt (step nt is the PV-only MFMA phase): step 0, a main
-        // loop of three unconditional steps a trip, then the last two to four
+        if (g == 1) __builtin_amdgcn_s_barrier();
         step<0, false>(0);
         int u = 1;
         for (; u + 4 < nt; u += 3) {
@@ -567,32 +611,36 @@ struct AttnPP {
             if (u + 2 <= nt) step<0, false>(u + 2);
         }
         if (g == 0) __builtin_amdgcn_s_barrier();
-        // out[q][h * 128 + d] = O^T[d][q] / l * 2 sigmoid(glog[q][h]), through
-        // a wave-private LDS patch [32 q][64 d] (row pitch 72 elements,
-        // 144 B) per half of d so that every global store is 16 contiguous
-        // bytes of a row.
-        // All waves have passed their last barrier: the stages are free.
-        const int hh = lane >> 5, r = lane & 31;
-        const float lt = l + __shfl_xor(l, 32, 64);
-        const int qr = q0 + r;
-        const float gg = (a.glog && qr < lq) ? 2.0f * sigmoid_f(a.glog[(size_t)qr * LTX_H + h]) : 1.0f;
-        const float sc = gg / lt;
+        // out[q][h * 128 + d] = O^T[d][q] / l * 2 sigmoid(glog[q][h]) through a
+        // wave-private LDS patch [32 q][64 d] (pitch 72 elements) per half of d
+        const int j = lane >> 4, r = lane & 15;
+        float sc[2];
+        bool qok[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++) {
+            float lt = l[qb] + __shfl_xor(l[qb], 16, 64);
+            lt += __shfl_xor(lt, 32, 64);
+            const int q = q0 + 16 * qb + r;
+            qok[qb] = q < lq;
+            const float gg = (a.glog && qok[qb]) ? 2.0f * sigmoid_f(a.glog[(size_t)q * LTX_H + h]) : 1.0f;
+            sc[qb] = gg / lt;
+        }
         uint16_t* patch = (uint16_t*)(w < 3 ? app_k0 + 4608 * w : w < 6 ? app_k1 + 4608 * (w - 3) : app_k2 + 4608 * (w - 6));
         uint16_t* out = (uint16_t*)a.out;
         unsigned bad = 0;  // 16-bit outputs out of range (range guard)
 #pragma unroll
         for (int half = 0; half < 2; half++) {
 #pragma unroll
-            for (int dbh = 0; dbh < 2; dbh++) {
-                const int db = 2 * half + dbh;
+            for (int dbh = 0; dbh < 4; dbh++) {
+                const int db = 4 * half + dbh;
 #pragma unroll
-                for (int rg = 0; rg < 4; rg++) {
-                    const int d = 32 * dbh + 8 * rg + 4 * hh;  // within this half
-                    *(u32x2*)(patch + r * 72 + d) =
-                        u32x2{Op<T>::cvt2(o[db][4 * rg] * sc, o[db][4 * rg + 1] * sc),
-                              Op<T>::cvt2(o[db][4 * rg + 2] * sc, o[db][4 * rg + 3] * sc)};
+                for (int qb = 0; qb < 2; qb++) {
+                    const f32x4 v = o[db][qb] * sc[qb];
+                    *(u32x2*)(patch + (16 * qb + r) * 72 + 16 * dbh + 4 * j) =
+                        u32x2{Op<T>::cvt2(v[0], v[1]), Op<T>::cvt2(v[2], v[3])};
+                    if (qok[qb])
 #pragma unroll
-                    for (int e = 0; e < 4; e++) bad += out_of_range<T>(o[db][4 * rg + e] * sc);
+                        for (int e = 0; e < 4; e++) bad += out_of_range<T>(v[e]);
                 }
             }
 #pragma unroll
@@ -603,7 +651,7 @@ struct AttnPP {
                 if (q < lq) *(u32x4*)(out + (size_t)q * LTX_D + h * LTX_HD + 64 * half + 8 * c) = v;
             }
         }
-        range_report(a.sat, qr < lq ? bad : 0u);
+        range_report(a.sat, bad);
     }
 };
 

@@ -35,6 +35,9 @@ struct Op<_Float16> {
     static __device__ __forceinline__ f32x16 mfma32(v8 a, v8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
     }
+    static __device__ __forceinline__ f32x4 mfma16(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
     // two f32 -> packed pair, one v_cvt_pk_f16_f32 (round to nearest even)
     static __device__ __forceinline__ uint32_t cvt2(float a, float b) {
         return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
@@ -64,6 +67,9 @@ struct Op<__bf16> {
     }
     static __device__ __forceinline__ f32x16 mfma32(v8 a, v8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 mfma16(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
     }
     static __device__ __forceinline__ uint32_t cvt2(float a, float b) {
         return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
