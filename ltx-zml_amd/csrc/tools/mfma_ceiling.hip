@@ -1,7 +1,9 @@
 // Practical MFMA ceiling of one MI355X: the rate of v_mfma_f32_32x32x16_{f16,bf16}
 // loops on random operands, with the A operand from registers, from one
-// ds_read_b128 per MFMA (the attention's fragment rate) or from one read per
-// two MFMAs. The published dense peak assumes the top clock; under a
+// ds_read_b128 per MFMA (the GEMMs' and the 32x32x16 attention's fragment
+// rate) or from one read per two MFMAs; and of v_mfma_f32_16x16x32_f16 (the
+// attention's shape) from registers and from one read per two MFMAs (the same
+// LDS bytes per flop as one read per 32x32x16). The published dense peak assumes the top clock; under a
 // sustained MFMA load the board's power limit sets a lower clock, and that
 // clock depends on the operand type and on the operands' bits.
 //
@@ -23,6 +25,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 enum { SRC_REGS = 0, SRC_LDS = 1, SRC_LDS_HALF = 2 };
 
@@ -92,6 +95,46 @@ __global__ void __launch_bounds__(512) ceiling(float* out, int iters) {
     out[(size_t)blockIdx.x * 512 + threadIdx.x] = t;
 }
 
+// 16x16x32 f16: 32 MFMAs per iteration (the flops of 16 of 32x32x16) over
+// eight accumulators; SRC_LDS_HALF reads one fragment per two MFMAs
+template <int SRC>
+__global__ void __launch_bounds__(512) ceiling16(float* out, int iters) {
+    __shared__ u32x4 lds[6144];  // 96 KB: one workgroup per CU
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for (int i = threadIdx.x; i < 1024; i += 512)
+        lds[i] = u32x4{rand_pair<false>(4 * i), rand_pair<false>(4 * i + 1), rand_pair<false>(4 * i + 2),
+                       rand_pair<false>(4 * i + 3)};
+    __syncthreads();
+    const uint32_t s0 = 4096u + 8u * (uint32_t)lane;
+    const f16x8 b = __builtin_bit_cast(f16x8, u32x4{rand_pair<false>(s0), rand_pair<false>(s0 + 1),
+                                                    rand_pair<false>(s0 + 2), rand_pair<false>(s0 + 3)});
+    const f16x8 areg = __builtin_bit_cast(f16x8, u32x4{rand_pair<false>(s0 + 4), rand_pair<false>(s0 + 5),
+                                                       rand_pair<false>(s0 + 6), rand_pair<false>(s0 + 7)});
+    f32x4 acc[8];
+    for (int i = 0; i < 8; i++)
+        for (int e = 0; e < 4; e++) acc[i][e] = 0.0f;
+    auto load = [&](int q) -> f16x8 {
+        if (SRC == SRC_REGS) return areg;
+        return __builtin_bit_cast(f16x8, lds[((w + q) & 15) * 64 + lane]);
+    };
+    f16x8 fr[4];
+    for (int j = 0; j < 4; j++) fr[j] = load(j);
+    int q = 4;
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const int f = (j >> 1) & 3;
+            acc[j & 7] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fr[f], b, acc[j & 7], 0, 0, 0);
+            if (SRC != SRC_REGS && (j & 1)) fr[f] = load(q++);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    float t = 0.0f;
+    for (int i = 0; i < 8; i++)
+        for (int e = 0; e < 4; e++) t += acc[i][e];
+    out[(size_t)blockIdx.x * 512 + threadIdx.x] = t;
+}
+
 struct Variant {
     const char* name;
     void (*kern)(float*, int);
@@ -108,6 +151,7 @@ int main(int argc, char** argv) {
         {"f16_regs", ceiling<false, SRC_REGS>},         {"f16_lds_per_mfma", ceiling<false, SRC_LDS>},
         {"f16_lds_per_2mfma", ceiling<false, SRC_LDS_HALF>}, {"bf16_regs", ceiling<true, SRC_REGS>},
         {"bf16_lds_per_mfma", ceiling<true, SRC_LDS>},   {"bf16_lds_per_2mfma", ceiling<true, SRC_LDS_HALF>},
+        {"f16_16x16x32_regs", ceiling16<SRC_REGS>},      {"f16_16x16x32_lds_per_2mfma", ceiling16<SRC_LDS_HALF>},
     };
     hipEvent_t e0, e1;
     if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return 1;
