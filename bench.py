@@ -393,6 +393,9 @@ def main() -> int:
     ap.add_argument("--denoise", type=int, default=0, metavar="BLOCKS",
                     help="instead of the block line: time the stage-1 denoising loop (8 Euler steps) over this "
                          "many resident blocks (48 for the whole transformer) and print its own JSON line")
+    ap.add_argument("--weights", default="int8", choices=["int8", "bf16"],
+                    help="int8: all seven projections int8 grouped-128 (the benchmark configuration); bf16: the "
+                         "unquantised block of the reference's production pass (Block.wBlockOut)")
     ap.add_argument("--scales", default="f16", choices=["f16", "f32"],
                     help="scale type of the int8 weights: fp16 (the benchmark configuration) or f32 (the "
                          "reference packer's version-1 format)")
@@ -428,7 +431,8 @@ def main() -> int:
     if args.sweep:
         return sweep_bench(args)
     t0 = time.time()
-    bt = synth.make_block(0, seed=1, dist="t3", classes=("qkv", "ff", "out"), scale_dtype=args.scales.upper())
+    bt = synth.make_block(0, seed=1, dist="t3", classes=("qkv", "ff", "out") if args.weights == "int8" else (),
+                          scale_dtype=args.scales.upper())
     inp = synth.make_inputs(T, S, sigma=0.7)
     cos, sin = rt.rope_tables(inp["grid"])
     log(f"bench: inputs ready in {time.time() - t0:.1f}s (T={T}, S={S})")
@@ -485,7 +489,8 @@ def main() -> int:
         "ms_per_step": round(ms, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16" if args.mode == "f16" else "bf16",
-        "weights": "int8 grouped-128, " + ("fp16" if args.scales == "f16" else "f32") + " scales",
+        "weights": ("int8 grouped-128, " + ("fp16" if args.scales == "f16" else "f32") + " scales")
+                   if args.weights == "int8" else "bf16 (unquantised)",
         "data": "synthetic",
         "config": {"workload": "LTX-2.5 DiT block forward, int8 weights", "tokens": T, "latent_grid": [14, 32, 64],
                    "text_tokens": S, "d_model": D, "heads": H, "head_dim": HD, "ffn": FF, "sigma": 0.7,
@@ -494,6 +499,12 @@ def main() -> int:
         "pct_bf16_dense_peak": round(100.0 * total / (ms * 1e-3) / 1e12 / PEAK_TFLOPS, 2),
         "attention_tflops": round(achieved, 1),
         "gemm_tflops": round(f["gemm"] / (gemm_ms * 1e-3) / 1e12, 1) if gemm_ms else None,
+        # the GEMMs' and attention's flops (the gate logits, on the second
+        # stream, left out) over their summed launch times (split-K reduce
+        # included): the MFMA kernels' share of the peak
+        "gemm_attn_pct_peak": round(100.0 * (total - 4 * T * D * H)
+                                    / ((gemm_ms + per["splitk_reduce"] + attn_ms + per["attn:cross"]) * 1e-3)
+                                    / 1e12 / PEAK_TFLOPS, 2),
         "kernel_ms": per,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS, 4),

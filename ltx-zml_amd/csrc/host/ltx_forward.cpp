@@ -31,11 +31,11 @@ struct Ws16 {
         *kh2, *o2, *x_ca, *ff_in, *h, *part;
 };
 
-// Split-K slices of a GEMM whose 256 x 256 output tiles would fill at most
+// Split-K slices of a GEMM whose 256 x tn output tiles would fill at most
 // half the CUs: the largest power of two S <= 8 with tiles * S <= CUs and
 // K / S a multiple of 128 of at least 512 (eight K-tiles per slice).
-static int gemm_ksplit(int num_cu, int M, int N, int K) {
-    const int tiles = ((M + 255) / 256) * (N / 256);
+static int gemm_ksplit(int num_cu, int M, int N, int K, int tn = 256) {
+    const int tiles = ((M + 255) / 256) * (N / tn);
     int s = 1;
     while (s < 8 && tiles * s * 2 <= num_cu && K % (256 * s) == 0 && K / (s * 2) >= 512) s *= 2;
     return s;
@@ -158,7 +158,6 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
         g.b = mode == LTX_MODE_BF16 ? p.w_bf16.p : p.w_f16.p;
         g.scales = nullptr;
         bk = "w16";
-        if (epi == LTX_EPI_QKV) throw Error("gemm16: the QKV epilogue needs int8 weights");
     }
     if (!g.b) throw Error("gemm16: weight not resident for this mode");
     g.tiles_m = (M + 255) / 256;
@@ -187,6 +186,22 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
         return;
     }
     const char* es = epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv";
+    // LDS-DMA 16-bit-weight kernel (256 x 128 tiles): the same conditions
+    if ((mode == LTX_MODE_F16 || mode == LTX_MODE_BF16) && !p.q8 && c->gemm_dma && p.K % 128 == 0 &&
+        p.N % 128 == 0 && (uint64_t)M * lda * 2 < (1ull << 31) && (uint64_t)p.N * p.K * 2 < (1ull << 31) &&
+        g.ldo % 8 == 0 && al16(g.out) && al16(g.out2) && al16(g.resid) && al16(g.bias) && al16(g.ada.tstab) &&
+        al16(g.ada.sst) && al16(g.b)) {
+        std::snprintf(name, sizeof(name), "ltx_gemm_w16dma_%s_%s", msuffix(mode), es);
+        g.tiles_n = p.N / 128;
+        g.ksplit = g.part ? gemm_ksplit(c->num_cu, M, p.N, p.K, 128) : 1;
+        const int nitems = g.tiles_m * g.tiles_n * g.ksplit;
+        c->launch(name, c->gemm_persistent ? std::min(nitems, c->num_cu) : nitems, 1, 1, 512, &g, st, label);
+        if (g.ksplit > 1) {
+            std::snprintf(name, sizeof(name), "ltx_gemm_reduce_%s_%s", msuffix(mode), es);
+            c->launch(name, p.N / 64, (M + 63) / 64, 1, 256, &g, st, "splitk_reduce");
+        }
+        return;
+    }
     std::snprintf(name, sizeof(name), "ltx_gemm_%s_%s_%s", msuffix(mode), bk, es);
     // split-K as above; the reduce kernel moves 16-byte vectors, so only with
     // aligned operands
@@ -365,7 +380,6 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
         return;
     }
 
-    if (!w->qkv1.q8 || !w->kv2.q8) throw Error("16-bit modes need int8 q/k/v weights (the QBlock recipe)");
     if (mode == LTX_MODE_F16 && !(w->f16_max <= 65504.0f))
         throw Error("mode F16: weight operands beyond the f16 range (largest |q s| or |w| " +
                     std::to_string(w->f16_max) + " > 65504); run LTX_MODE_BF16");

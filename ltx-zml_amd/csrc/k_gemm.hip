@@ -13,6 +13,7 @@
 // LDS rows are padded by 16 bytes.
 #include "gemm_common.h"
 #include "gemm_q8.h"
+#include "gemm_w16.h"
 
 #define BM 256
 #define BN 256
@@ -180,6 +181,7 @@ GEMM_KERNEL(ltx_gemm_f16_i8f16_resid, _Float16, LTX_B_I8_F16S, LTX_EPI_RESID_GAT
 GEMM_KERNEL(ltx_gemm_f16_i8f16_qkv, _Float16, LTX_B_I8_F16S, LTX_EPI_QKV)
 GEMM_KERNEL(ltx_gemm_f16_w16_store, _Float16, LTX_B_W16, LTX_EPI_STORE)
 GEMM_KERNEL(ltx_gemm_f16_w16_resid, _Float16, LTX_B_W16, LTX_EPI_RESID_GATE)
+GEMM_KERNEL(ltx_gemm_f16_w16_qkv, _Float16, LTX_B_W16, LTX_EPI_QKV)
 GEMM_KERNEL(ltx_gemm_bf16_i8f32_store, __bf16, LTX_B_I8_F32S, LTX_EPI_STORE)
 GEMM_KERNEL(ltx_gemm_bf16_i8f32_resid, __bf16, LTX_B_I8_F32S, LTX_EPI_RESID_GATE)
 GEMM_KERNEL(ltx_gemm_bf16_i8f32_qkv, __bf16, LTX_B_I8_F32S, LTX_EPI_QKV)
@@ -188,6 +190,7 @@ GEMM_KERNEL(ltx_gemm_bf16_i8f16_resid, __bf16, LTX_B_I8_F16S, LTX_EPI_RESID_GATE
 GEMM_KERNEL(ltx_gemm_bf16_i8f16_qkv, __bf16, LTX_B_I8_F16S, LTX_EPI_QKV)
 GEMM_KERNEL(ltx_gemm_bf16_w16_store, __bf16, LTX_B_W16, LTX_EPI_STORE)
 GEMM_KERNEL(ltx_gemm_bf16_w16_resid, __bf16, LTX_B_W16, LTX_EPI_RESID_GATE)
+GEMM_KERNEL(ltx_gemm_bf16_w16_qkv, __bf16, LTX_B_W16, LTX_EPI_QKV)
 
 // LDS-DMA W8A16 kernels (ping-pong schedule): ltx_gemm_q8_[bf16_][s32_]{store,
 // resid,qkv} for f16 (bf16_: bf16) operands with f16 (s32_: f32) scales.
@@ -203,6 +206,15 @@ Q8_GEMM_KERNEL(ltx_gemm_q8_s32_qkv, _Float16, true, LTX_EPI_QKV)
 Q8_GEMM_KERNEL(ltx_gemm_q8_bf16_s32_store, __bf16, true, LTX_EPI_STORE)
 Q8_GEMM_KERNEL(ltx_gemm_q8_bf16_s32_resid, __bf16, true, LTX_EPI_RESID_GATE)
 Q8_GEMM_KERNEL(ltx_gemm_q8_bf16_s32_qkv, __bf16, true, LTX_EPI_QKV)
+
+// LDS-DMA W16A16 kernels (unquantised weights): ltx_gemm_w16dma_{f16,bf16}_
+// {store,resid,qkv}, 256 x 128 output tiles.
+W16_GEMM_KERNEL(ltx_gemm_w16dma_f16_store, _Float16, LTX_EPI_STORE)
+W16_GEMM_KERNEL(ltx_gemm_w16dma_f16_resid, _Float16, LTX_EPI_RESID_GATE)
+W16_GEMM_KERNEL(ltx_gemm_w16dma_f16_qkv, _Float16, LTX_EPI_QKV)
+W16_GEMM_KERNEL(ltx_gemm_w16dma_bf16_store, __bf16, LTX_EPI_STORE)
+W16_GEMM_KERNEL(ltx_gemm_w16dma_bf16_resid, __bf16, LTX_EPI_RESID_GATE)
+W16_GEMM_KERNEL(ltx_gemm_w16dma_bf16_qkv, __bf16, LTX_EPI_QKV)
 
 // Gate logits (ltx/block.zig:238, 526, 564): glog[t][h] = a[t] . gw[h] + gb[h].
 // One wave per 32 token rows: 256 MFMAs over K = 4096, operands straight

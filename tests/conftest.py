@@ -30,6 +30,15 @@ def block0_out():
 
 
 @pytest.fixture(scope="session")
+def block0_w16():
+    """The same block unquantised (every projection in its bf16 weights): the
+    recipe of Block.wBlockOut (ltx/block.zig:351-353), the reference's
+    production caller (ltx/e2e_prod.zig:382-399)."""
+    from ltx_amd import synth
+    return synth.make_block(0, seed=1, dist="t3", classes=())
+
+
+@pytest.fixture(scope="session")
 def ctx():
     import torch
     from ltx_amd import runtime

@@ -53,6 +53,15 @@ def full_s32(full):
     return bt, inp, cos, sin
 
 
+@pytest.fixture(scope="module")
+def full_w16(full):
+    """The same block unquantised (every projection in bf16): Block.wBlockOut
+    (ltx/block.zig:351-353), the reference's production caller."""
+    _, inp, cos, sin = full
+    bt = synth.make_block(0, seed=1, dist="t3", classes=())
+    return bt, inp, cos, sin
+
+
 def _run(ctx, w, inp, cos, sin, mode=rt.MODE_F16):
     y = torch.empty((T, 4096), dtype=torch.float32, device="cuda")
     ctx.forward(w, dev(inp["x"]), dev(inp["tstab"]), dev(inp["tidx"]), dev(inp["ctx"]), dev(inp["pts2"]), dev(cos),
@@ -154,13 +163,15 @@ def _oracle_rows(key, bt, inp, cos, sin):
     return _ROW_ORACLE[key]
 
 
-@pytest.mark.parametrize("mode,scales", [("f16", "f16"), ("f16", "f32"), ("bf16", "f16")])
+@pytest.mark.parametrize("mode,scales", [("f16", "f16"), ("f16", "f32"), ("bf16", "f16"), ("f16", "w16"),
+                                         ("bf16", "w16")])
 def test_full_size_block_rows(ctx, request, mode, scales):
-    """The block at T = 28,672, S = 256, every projection int8: output rows,
+    """The block at T = 28,672, S = 256, every projection int8 (scales f16 or
+    f32) or every projection bf16 (w16, the unquantised block): output rows,
     and the self-attention, cross-attention and FFN residual branches of
     those rows, against the f64 oracle (gate 2e-3 with fp16 operands; bf16
     operands printed and held to 1.5e-2)."""
-    bt, inp, cos, sin = request.getfixturevalue("full" if scales == "f16" else "full_s32")
+    bt, inp, cos, sin = request.getfixturevalue({"f16": "full", "f32": "full_s32", "w16": "full_w16"}[scales])
     say(f"full-size block rows T={T} S={S} {mode} operands, {scales} scales")
     w = ctx.upload(bt)
     y = _run(ctx, w, inp, cos, sin, rt.MODES[mode])

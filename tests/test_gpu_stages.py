@@ -122,6 +122,34 @@ def test_block_stages(ctx, block0, mode, T, S):
     assert not bad, f"stages over the {GATE[mode]:.0e} gate: {bad}"
 
 
+@pytest.mark.parametrize("T,S", [(256, 64), (2048, 64)])
+@pytest.mark.parametrize("mode", ["f16", "bf16"])
+def test_unquantised_block_stages(ctx, block0_w16, mode, T, S):
+    """The unquantised block (Block.wBlockOut, ltx/block.zig:351-353: every
+    projection in bf16 weights, as the reference's production pass calls it,
+    ltx/e2e_prod.zig:382-399) in the 16-bit modes, every stage against the
+    oracle of the same weights. T = 256 runs the 16-bit-weight GEMMs split
+    over K, T = 2,048 whole (256 x 128 tiles fill the CUs). In mode F16 the
+    bf16 weights are exact f16 operands (8 significant bits, in range)."""
+    say(f"unquantised block stages mode={mode} T={T} S={S}")
+    inp = synth.make_inputs(T, S, sigma=0.7)
+    cos, sin = rt.rope_tables(inp["grid"])
+    key = ("w16", T, S)
+    if key not in _CACHE:
+        _CACHE[key] = oracle.block_forward(block0_w16, inp, cos, sin, chunk=64, stages=True)
+    want, wst = _CACHE[key]
+    w = ctx.upload(block0_w16)
+    y = forward(ctx, w, inp, cos, sin, mode)
+    g = gpu_stages(ctx, mode, T, S)
+    w.free()
+    r = compare_stages(g, y, want, wst, inp["x"].astype(np.float64))
+    say("  " + " ".join(f"{k}={v:.2e}" for k, v in r.items()))
+    bad = {k: v for k, v in r.items() if not v <= GATE[mode]}
+    assert not bad, f"stages over the {GATE[mode]:.0e} gate: {bad}"
+    if mode == "bf16":
+        assert r["y"] <= 2e-3
+
+
 @pytest.mark.parametrize("mode", ["f16", "f32"])
 def test_block_closed_form(ctx, block0, mode):
     """The special case of tests/blockcases.py on the GPU: every token's
