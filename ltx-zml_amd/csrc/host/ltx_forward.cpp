@@ -253,6 +253,16 @@ static void attn16(ltx_ctx* c, int mode, const void* q, const void* k, const voi
     a.scale_log2 = q_scaled ? 1.0f : kAttnC;
     a.q_tiles = (lq + 255) / 256;  // 256 queries per workgroup
     char name[48];
+    const int wph = std::max(1, std::min(c->num_cu / LTX_H, a.q_tiles));  // workgroups per head
+    if (c->attn_kv && lkv % 64 == 0 && lkv >= 64 && lkv <= 256 && (a.q_tiles >= 2 * wph || lkv < 128)) {
+        // resident K/V: each workgroup loads one head's K and V^T once and
+        // runs every wph-th query tile of that head (with fewer than two
+        // tiles per workgroup the streaming kernel, which overlaps the K/V
+        // loads with the first tiles, is faster)
+        std::snprintf(name, sizeof(name), "ltx_attn_%s_kv%s", msuffix(mode), q_scaled ? "" : "_uq");
+        c->launch(name, LTX_H * wph, 1, 1, 512, &a, st, label);
+        return;
+    }
     if (c->attn_pp && lkv % 64 == 0 && lkv >= 128) {
         // ping-pong kernel: whole 64-key tiles, at least two
         std::snprintf(name, sizeof(name), "ltx_attn_%s_pp%s", msuffix(mode), q_scaled ? "" : "_uq");

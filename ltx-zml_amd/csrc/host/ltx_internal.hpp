@@ -75,11 +75,14 @@ struct ltx_ctx {
     int device = 0;
     // kernel selection: the int8 GEMM's LDS-DMA ping-pong kernel (true) or
     // the register-staged one; the ping-pong attention for whole 64-key tiles
-    // (true) or the any-length kernel everywhere (both kept for testing)
+    // (true) or the any-length kernel everywhere; for 64-256 keys the
+    // resident-K/V form of the ping-pong kernel (true) or its streaming form
+    // (all kept for testing)
     bool gemm_dma = true;
     int num_cu = 256;             // compute units: the persistent GEMM's grid bound
     bool gemm_persistent = true;  // LDS-DMA GEMM: at most one workgroup per CU, looping over tiles
     bool attn_pp = true;
+    bool attn_kv = true;
     // side stream of a forward: work off the main chain (gate logits, the
     // cross-attention K/V) overlaps it, ordered by the events
     hipStream_t side = nullptr;

@@ -160,10 +160,14 @@ int ltx_init(int device, ltx_ctx** out) {
         // LTX_GEMM_GRID=tile: one workgroup per output tile instead of the
         // persistent grid of one per CU; LTX_GEMM_Q8=reg: the register-staged
         // int8 GEMM everywhere; LTX_ATTN_VARIANT=w8: the any-length attention
-        // everywhere (the kernels each test exercises beside the defaults)
+        // everywhere, =pp: the streaming ping-pong attention also for 64-256
+        // keys (the kernels each test exercises beside the defaults)
         if (const char* e = std::getenv("LTX_GEMM_GRID")) c->gemm_persistent = std::strcmp(e, "tile") != 0;
         if (const char* e = std::getenv("LTX_GEMM_Q8")) c->gemm_dma = std::strcmp(e, "reg") != 0;
-        if (const char* e = std::getenv("LTX_ATTN_VARIANT")) c->attn_pp = std::strcmp(e, "w8") != 0;
+        if (const char* e = std::getenv("LTX_ATTN_VARIANT")) {
+            c->attn_pp = std::strcmp(e, "w8") != 0;
+            c->attn_kv = c->attn_pp && std::strcmp(e, "pp") != 0;
+        }
         HIPC(hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking));  // default priority
         for (auto& e : c->side_ev) HIPC(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         for (const unsigned char* co : {ltx_co_k_gemm, ltx_co_k_attn, ltx_co_k_norm, ltx_co_k_f32, ltx_co_k_core}) {

@@ -391,12 +391,10 @@ struct AttnPP {
                                                          t * 128 + 128 * a.lkv * h, 0, 0);
     }
 
-    // MFMA phase t: PV(t-1) from V stage VS, then S(t) from K stage KS; each
-    // fragment feeds the MFMAs of both query blocks
-    template <int KS, int VS>
-    __device__ __forceinline__ void mfma_phase(bool ds, bool dp) {
+    // MFMA phase t: PV(t-1) from the V^T tile at sv, then S(t) from the K tile
+    // at sk; each fragment feeds the MFMAs of both query blocks
+    __device__ __forceinline__ void mfma_phase(const uint8_t* sk, const uint8_t* sv, bool ds, bool dp) {
         if (dp) {
-            const uint8_t* sv = app_v<VS>();
 #pragma unroll
             for (int kc = 0; kc < 2; kc++)
 #pragma unroll
@@ -407,7 +405,6 @@ struct AttnPP {
                 }
         }
         if (ds) {
-            const uint8_t* sk = app_k<KS>();
 #pragma unroll
             for (int kb = 0; kb < 4; kb++) {
                 s[kb][0] = sb[0];
@@ -510,7 +507,7 @@ struct AttnPP {
     template <int T3, bool FULL>
     __device__ __forceinline__ void step(int t) {
         __builtin_amdgcn_s_setprio(1);
-        mfma_phase<T3, (T3 + 2) % 3>(FULL || t < nt, FULL || t >= 1);
+        mfma_phase(app_k<T3>(), app_v<(T3 + 2) % 3>(), FULL || t < nt, FULL || t >= 1);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
         barrier();
@@ -540,19 +537,11 @@ struct AttnPP {
         barrier();
     }
 
-    __device__ __forceinline__ void run() {
-        const int tid = threadIdx.x, lane = tid & 63;
-        const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-        g = w >> 2;
-        const int nblk = a.q_tiles * LTX_H;
-        int t = blockIdx.x;
-        if ((nblk & 7) == 0) t = (t & 7) * (nblk >> 3) + (t >> 3);
-        const int h = t / a.q_tiles, qt = t - h * a.q_tiles;
-        const int q0 = qt * 256 + w * 32;
-        const int lq = a.lq, lkv = a.lkv;
+    // Buffers, DMA sources and fragment offsets of head h (wave w)
+    __device__ __forceinline__ void setup(int h, int w, int lane) {
+        const int lkv = a.lkv;
         nt = lkv / 64;
         C = a.scale_log2;
-        const uint16_t* Q = (const uint16_t*)a.q + (size_t)h * lq * LTX_HD;
         rk = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint16_t*)a.k + (size_t)h * lkv * LTX_HD), 0,
                                                lkv * LTX_HD * 2, ASP_RSRC_W3);
         rv = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint16_t*)a.vt + (size_t)h * LTX_HD * lkv), 0,
@@ -571,25 +560,100 @@ struct AttnPP {
             const int cv = (lane & 7) ^ ((d >> 1) & 7);
             gv[i] = (uint32_t)d * (uint32_t)lkv * 2u + 16u * cv;
         }
-        {
-            const int j = lane >> 4, r = lane & 15;
+        const int j = lane >> 4, r = lane & 15;
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) ok[ks] = r * 256 + 16 * ((4 * ks + j) ^ r);
+        for (int ks = 0; ks < 4; ks++) ok[ks] = r * 256 + 16 * ((4 * ks + j) ^ r);
 #pragma unroll
-            for (int kc = 0; kc < 2; kc++) ov[kc] = r * 128 + 16 * ((4 * kc + j) ^ (r >> 1));
+        for (int kc = 0; kc < 2; kc++) ov[kc] = r * 128 + 16 * ((4 * kc + j) ^ (r >> 1));
+    }
+
+    // Q^T operands of the wave's queries q0 .. q0 + 31 of head h (rows past
+    // lq read row lq - 1)
+    __device__ __forceinline__ void load_q(v8 (&dst)[2][4], int h, int q0, int lane) const {
+        const uint16_t* Q = (const uint16_t*)a.q + (size_t)h * a.lq * LTX_HD;
+        const int j = lane >> 4, r = lane & 15;
 #pragma unroll
-            for (int qb = 0; qb < 2; qb++) {
-                const int q = min(q0 + 16 * qb + r, lq - 1);
+        for (int qb = 0; qb < 2; qb++) {
+            const int q = min(q0 + 16 * qb + r, a.lq - 1);
 #pragma unroll
-                for (int ks = 0; ks < 4; ks++)
-                    qf[qb][ks] = __builtin_bit_cast(v8, *(const u32x4*)(Q + (size_t)q * LTX_HD + 32 * ks + 8 * j));
-            }
+            for (int ks = 0; ks < 4; ks++)
+                dst[qb][ks] = __builtin_bit_cast(v8, *(const u32x4*)(Q + (size_t)q * LTX_HD + 32 * ks + 8 * j));
         }
+    }
+
+    __device__ __forceinline__ void reset() {
 #pragma unroll
         for (int db = 0; db < 8; db++) o[db][0] = o[db][1] = f32x4{0};
         m = f32x2{0.f, 0.f};
         sb[0] = sb[1] = f32x4{0};
         l = f32x2{0.f, 0.f};
+    }
+
+    // gate logits glog[q][h] of the lane's two queries (rows past lq read
+    // row lq - 1; gl is left as it is without gate)
+    __device__ __forceinline__ void load_glog(float (&gl)[2], int h, int q0, int lane) const {
+        if (a.glog)
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++)
+                gl[qb] = a.glog[(size_t)min(q0 + 16 * qb + (lane & 15), a.lq - 1) * LTX_H + h];
+    }
+
+    // out[q][h * 128 + d] = O^T[d][q] / l * 2 sigmoid(glog[q][h]) for the
+    // wave's queries q0 .. q0 + 31, through a wave-private LDS patch
+    // [32 q][DPP d] (pitch DPP + 8 elements) per DPP dims
+    template <int DPP>
+    __device__ __forceinline__ void store_out(uint16_t* patch, int h, int q0, int lane, const float (&gl)[2],
+                                              unsigned& bad) const {
+        constexpr int LD = DPP + 8, LPR = DPP / 8, RPI = 64 / LPR;  // lanes per row, rows per instruction
+        const int j = lane >> 4, r = lane & 15;
+        float sc[2];
+        bool qok[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++) {
+            float lt = l[qb] + __shfl_xor(l[qb], 16, 64);
+            lt += __shfl_xor(lt, 32, 64);
+            qok[qb] = q0 + 16 * qb + r < a.lq;
+            const float gg = a.glog ? 2.0f * sigmoid_f(gl[qb]) : 1.0f;
+            sc[qb] = gg / lt;
+        }
+        uint16_t* out = (uint16_t*)a.out;
+#pragma unroll
+        for (int part = 0; part < 128 / DPP; part++) {
+#pragma unroll
+            for (int dbh = 0; dbh < DPP / 16; dbh++) {
+                const int db = (DPP / 16) * part + dbh;
+#pragma unroll
+                for (int qb = 0; qb < 2; qb++) {
+                    const f32x4 v = o[db][qb] * sc[qb];
+                    *(u32x2*)(patch + (16 * qb + r) * LD + 16 * dbh + 4 * j) =
+                        u32x2{Op<T>::cvt2(v[0], v[1]), Op<T>::cvt2(v[2], v[3])};
+                    if (qok[qb])
+#pragma unroll
+                        for (int e = 0; e < 4; e++) bad += out_of_range<T>(v[e]);
+                }
+            }
+#pragma unroll
+            for (int it = 0; it < 32 / RPI; it++) {
+                const int row = RPI * it + lane / LPR, c = lane % LPR;  // LPR lanes x 16 B per row
+                const u32x4 v = *(const u32x4*)(patch + row * LD + 8 * c);
+                const int q = q0 + row;
+                if (q < a.lq) *(u32x4*)(out + (size_t)q * LTX_D + h * LTX_HD + DPP * part + 8 * c) = v;
+            }
+        }
+    }
+
+    __device__ __forceinline__ void run() {
+        const int tid = threadIdx.x, lane = tid & 63;
+        const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+        g = w >> 2;
+        const int nblk = a.q_tiles * LTX_H;
+        int t = blockIdx.x;
+        if ((nblk & 7) == 0) t = (t & 7) * (nblk >> 3) + (t >> 3);
+        const int h = t / a.q_tiles, qt = t - h * a.q_tiles;
+        const int q0 = qt * 256 + w * 32;
+        setup(h, w, lane);
+        load_q(qf, h, q0, lane);
+        reset();
         if (g == 0) {
             dma_k<0>(0);
             dma_k<1>(1);
@@ -611,46 +675,129 @@ struct AttnPP {
             if (u + 2 <= nt) step<0, false>(u + 2);
         }
         if (g == 0) __builtin_amdgcn_s_barrier();
-        // out[q][h * 128 + d] = O^T[d][q] / l * 2 sigmoid(glog[q][h]) through a
-        // wave-private LDS patch [32 q][64 d] (pitch 72 elements) per half of d
-        const int j = lane >> 4, r = lane & 15;
-        float sc[2];
-        bool qok[2];
-#pragma unroll
-        for (int qb = 0; qb < 2; qb++) {
-            float lt = l[qb] + __shfl_xor(l[qb], 16, 64);
-            lt += __shfl_xor(lt, 32, 64);
-            const int q = q0 + 16 * qb + r;
-            qok[qb] = q < lq;
-            const float gg = (a.glog && qok[qb]) ? 2.0f * sigmoid_f(a.glog[(size_t)q * LTX_H + h]) : 1.0f;
-            sc[qb] = gg / lt;
-        }
+        // every wave has passed its last barrier: the K stages hold the
+        // wave-private patches
         uint16_t* patch = (uint16_t*)(w < 3 ? app_k0 + 4608 * w : w < 6 ? app_k1 + 4608 * (w - 3) : app_k2 + 4608 * (w - 6));
-        uint16_t* out = (uint16_t*)a.out;
         unsigned bad = 0;  // 16-bit outputs out of range (range guard)
+        float gl[2] = {0.f, 0.f};
+        load_glog(gl, h, q0, lane);
+        store_out<64>(patch, h, q0, lane, gl, bad);
+        range_report(a.sat, bad);
+    }
+
+    // Resident K/V (lkv = 64 nt, 1 <= nt <= 4): the workgroup loads head h's
+    // whole K and V^T into LDS once (kres, vres: nt tiles of 16 KB each, the
+    // stage layouts above), then runs query tiles qt0, qt0 + wph, ... of that
+    // head with no DMA, as one continuous ping-pong over the (query tile, key
+    // tile) sequence: the MFMA phase after the last softmax of tile i runs
+    // PV_i(nt - 1) and S_i+1(0), and tile i's output is stored in the next
+    // softmax phase, before softmax_i+1(0) clears O and l. The running max
+    // and the Q^T operands switch to tile i + 1 at the end of softmax_i(nt -
+    // 1). The next tile's Q and the tile's gate logits load while it runs.
+    // Every query tile takes 2 nt barriers in both groups (group 1 keeps its
+    // one-phase lag), plus one after the final PV.
+    // the softmax phase's results stay in registers (not rematerialised in
+    // the next phase)
+    __device__ __forceinline__ void pin_softmax() {
 #pragma unroll
-        for (int half = 0; half < 2; half++) {
+        for (int kc = 0; kc < 2; kc++)
 #pragma unroll
-            for (int dbh = 0; dbh < 4; dbh++) {
-                const int db = 4 * half + dbh;
+            for (int qb = 0; qb < 2; qb++) asm volatile("" ::"v"(__builtin_bit_cast(u32x4, pf[kc][qb])));
+        asm volatile("" ::"v"(l), "v"(m));
+        asm volatile("" ::"v"(sb[0]), "v"(sb[1]));
+    }
+
+    // after the last softmax of a query tile: the next MFMA phase starts the
+    // next tile (S(0) from a zero max, with its Q)
+    __device__ __forceinline__ void next_tile(const v8 (&qn)[2][4]) {
+        m = f32x2{0.f, 0.f};
+        sb[0] = sb[1] = f32x4{0};
 #pragma unroll
-                for (int qb = 0; qb < 2; qb++) {
-                    const f32x4 v = o[db][qb] * sc[qb];
-                    *(u32x2*)(patch + (16 * qb + r) * 72 + 16 * dbh + 4 * j) =
-                        u32x2{Op<T>::cvt2(v[0], v[1]), Op<T>::cvt2(v[2], v[3])};
-                    if (qok[qb])
+        for (int qb = 0; qb < 2; qb++)
 #pragma unroll
-                        for (int e = 0; e < 4; e++) bad += out_of_range<T>(v[e]);
-                }
-            }
+            for (int ks = 0; ks < 4; ks++) qf[qb][ks] = qn[qb][ks];
+    }
+
+    __device__ __forceinline__ void rphase(const uint8_t* sk, const uint8_t* sv, bool ds, bool dp) {
+        __builtin_amdgcn_s_setprio(1);
+        mfma_phase(sk, sv, ds, dp);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+        barrier();
+    }
+
+    __device__ __forceinline__ void run_resident(uint8_t* kres, uint8_t* vres, uint16_t* patches) {
+        const int tid = threadIdx.x, lane = tid & 63;
+        const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+        g = w >> 2;
+        const int wph = gridDim.x / LTX_H;  // workgroups per head
+        const int h = blockIdx.x / wph, qt0 = blockIdx.x - h * wph;
+        if (h >= LTX_H || qt0 >= a.q_tiles) return;  // uniform over the workgroup
+        setup(h, w, lane);
+        // group 0 loads every K and V^T tile (its slices and group 1's)
+        if (g == 0) {
+            for (int t = 0; t < nt; t++) {
 #pragma unroll
-            for (int it = 0; it < 4; it++) {
-                const int row = 8 * it + (lane >> 3), c = lane & 7;  // 8 lanes x 16 B per row
-                const u32x4 v = *(const u32x4*)(patch + row * 72 + 8 * c);
-                const int q = q0 + row;
-                if (q < lq) *(u32x4*)(out + (size_t)q * LTX_D + h * LTX_HD + 64 * half + 8 * c) = v;
+                for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                    for (int i = 0; i < 2; i++) {
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                            rk, (attn_lds_ptr)(kres + 16384 * t + lw + 8192 * hh + 1024 * i), 16, gk[i],
+                            t * 16384 + 8192 * hh, 0, 0);
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                            rv, (attn_lds_ptr)(vres + 16384 * t + lw + 8192 * hh + 1024 * i), 16, gv[i],
+                            t * 128 + 128 * a.lkv * hh, 0, 0);
+                    }
             }
         }
+        int q0 = qt0 * 256 + w * 32;
+        load_q(qf, h, q0, lane);
+        float gl[2] = {0.f, 0.f};  // gate logits of the tile being computed, until its output is stored
+        load_glog(gl, h, q0, lane);
+        reset();
+        __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(0));
+        __builtin_amdgcn_s_barrier();
+        if (g == 1) __builtin_amdgcn_s_barrier();
+        uint16_t* patch = patches + 1280 * w;  // [32 q][40]: 32 dims per pass
+        unsigned bad = 0;  // 16-bit outputs out of range (range guard)
+        v8 qn[2][4];       // the next tile's Q^T operands
+        for (int qt = qt0; qt < a.q_tiles; qt += wph) {
+            const bool prev = qt > qt0;
+            // t = 0: PV of the previous tile's last key tile, S(0); then the
+            // previous tile's output, this tile's gate logits and the next
+            // tile's Q (read at t = nt - 1)
+            rphase(kres, vres + 16384 * (nt - 1), true, prev);
+            // unconditional (rows past lq read row lq - 1), so that every
+            // path waits for these loads where qf takes them; issued before
+            // the output stores, which would otherwise queue ahead of them
+            load_q(qn, h, q0 + 256 * wph, lane);
+            if (prev) {
+                store_out<32>(patch, h, q0 - 256 * wph, lane, gl, bad);
+                load_glog(gl, h, q0, lane);
+            }
+            softmax(true);
+            if (nt == 1) next_tile(qn);
+            pin_softmax();
+            barrier();
+            for (int t = 1; t < nt - 1; t++) {
+                rphase(kres + 16384 * t, vres + 16384 * (t - 1), true, true);
+                softmax(false);
+                pin_softmax();
+                barrier();
+            }
+            if (nt > 1) {
+                rphase(kres + 16384 * (nt - 1), vres + 16384 * (nt - 2), true, true);
+                softmax(false);
+                next_tile(qn);
+                pin_softmax();
+                barrier();
+            }
+            q0 += 256 * wph;
+        }
+        // the last tile's last PV, then its output
+        rphase(kres, vres + 16384 * (nt - 1), false, true);
+        store_out<32>(patch, h, q0 - 256 * wph, lane, gl, bad);
+        if (g == 0) __builtin_amdgcn_s_barrier();
         range_report(a.sat, bad);
     }
 };
@@ -671,4 +818,26 @@ extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_f16_pp_uq(const Lt
 extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_bf16_pp_uq(const LtxAttnArgs a) {
     AttnPP<__bf16, false> k(a);
     k.run();
+}
+
+// _kv: resident K/V (a multiple of 64 keys, at most 256), persistent over
+// query tiles: grid = LTX_H x workgroups per head
+__shared__ __attribute__((aligned(1024))) uint8_t arx_k[65536];
+__shared__ __attribute__((aligned(1024))) uint8_t arx_v[65536];
+__shared__ __attribute__((aligned(1024))) uint16_t arx_patch[8 * 1280];
+extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_f16_kv(const LtxAttnArgs a) {
+    AttnPP<_Float16, true> k(a);
+    k.run_resident(arx_k, arx_v, arx_patch);
+}
+extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_bf16_kv(const LtxAttnArgs a) {
+    AttnPP<__bf16, true> k(a);
+    k.run_resident(arx_k, arx_v, arx_patch);
+}
+extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_f16_kv_uq(const LtxAttnArgs a) {
+    AttnPP<_Float16, false> k(a);
+    k.run_resident(arx_k, arx_v, arx_patch);
+}
+extern "C" __global__ void __launch_bounds__(512, 1) ltx_attn_bf16_kv_uq(const LtxAttnArgs a) {
+    AttnPP<__bf16, false> k(a);
+    k.run_resident(arx_k, arx_v, arx_patch);
 }

@@ -200,7 +200,10 @@ def _heads(x, L):  # [L, D] -> [H, L, 128]
                                           (64, 77, True),
                                           # the ping-pong kernel's shortest loop (two 64-key tiles) and
                                           # key counts the any-length kernel masks
-                                          (100, 128, True), (300, 160, True), (256, 480, False)])
+                                          (100, 128, True), (300, 160, True), (256, 480, False),
+                                          # resident K/V (64-256 keys): several query tiles per workgroup,
+                                          # a ragged last tile, one to four key tiles
+                                          (4000, 256, True), (3000, 64, True), (2100, 192, False)])
 @pytest.mark.parametrize("q_scaled", [False, True])
 def test_attention(ctx, mode, lq, lkv, gated, q_scaled):
     """q_scaled: q arrives multiplied by log2(e)/sqrt(128), as the block's
@@ -277,16 +280,21 @@ def test_attention_special_cases(ctx, lkv, dom, q_scaled):
     assert np.abs(f64(out) - vd[None, :]).max() < 5e-3
 
 
-@pytest.mark.parametrize("variant", ["w8", "pp"])
-def test_attention_variants(monkeypatch, variant):
-    """The any-length attention kernel forced everywhere (w8) and the default
-    (pp) against the dense f64 oracle on one case."""
-    say(f"attention variant={variant} lq=384 lkv=2048")
-    monkeypatch.setenv("LTX_ATTN_VARIANT", variant)
+@pytest.mark.parametrize("variant,lq,lkv", [("w8", 384, 2048), ("default", 384, 2048), ("pp", 1000, 256),
+                                            ("default", 1000, 256)])
+def test_attention_variants(monkeypatch, variant, lq, lkv):
+    """The any-length attention kernel forced everywhere (w8), the streaming
+    ping-pong kernel forced for 256 keys (pp) and the defaults (streaming
+    ping-pong for 2048 keys, resident K/V for 256) against the dense f64
+    oracle."""
+    say(f"attention variant={variant} lq={lq} lkv={lkv}")
+    if variant == "default":
+        monkeypatch.delenv("LTX_ATTN_VARIANT", raising=False)
+    else:
+        monkeypatch.setenv("LTX_ATTN_VARIANT", variant)
     c = rt.Context(0)
     try:
         rng = np.random.default_rng(21)
-        lq, lkv = 384, 2048
         q, k, v = (rng.standard_normal((n, 4096)).astype(np.float32) for n in (lq, lkv, lkv))
         glog = rng.standard_normal((lq, 32)).astype(np.float32)
         dt = torch.float16
