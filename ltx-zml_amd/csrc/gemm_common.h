@@ -94,30 +94,35 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
     const bool f32out = EPI == LTX_EPI_RESID_GATE || (EPI == LTX_EPI_STORE && a.out_f32);
     const int ldo = EPI == LTX_EPI_QKV ? a.nsplit : a.ldo;  // 16-bit rows: q | k [M][nsplit] or [M][ldo]
     unsigned bad = 0;  // 16-bit stores out of range (range guard)
+    // gated residual: lane rows r0 + RRPP p of each 32-row block, 4 columns
+    // each. The timestep rows of block i + 1 are loaded with block i's
+    // loads, so that a block's gate-row loads do not wait out a round trip
+    // for them.
+    constexpr int RLPR = WN / 4, RRPP = 64 / RLPR, RNP = 32 / RRPP;
+    constexpr int TNP = EPI == LTX_EPI_RESID_GATE ? RNP : 1;
+    int tixn[TNP];
+    if (EPI == LTX_EPI_RESID_GATE)
+#pragma unroll
+        for (int p = 0; p < TNP; p++) tixn[p] = ada_row(a.ada, min(mw + lane / RLPR + RRPP * p, a.M - 1));
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         const int mb = mw + 32 * i;
-        // gated residual: this block's residual rows and gate rows are loaded
-        // before anything is stored (the stores could alias them for the
-        // compiler, which would otherwise wait out one load round trip per
-        // row group)
-        constexpr int RLPR = WN / 4, RRPP = 64 / RLPR, RNP = 32 / RRPP;
-        f32x4 rs[EPI == LTX_EPI_RESID_GATE ? RNP : 1], gt[EPI == LTX_EPI_RESID_GATE ? RNP : 1];
+        // this block's residual rows and gate rows are loaded before
+        // anything is stored (the stores could alias them for the compiler,
+        // which would otherwise wait out one load round trip per row group)
+        f32x4 rs[TNP], gt[TNP];
         if (EPI == LTX_EPI_RESID_GATE) {
             const int c4 = 4 * (lane % RLPR), r0 = lane / RLPR;
             const int n = nw + c4;
-            int tix[RNP];
-#pragma unroll
-            for (int p = 0; p < RNP; p++) {
-                const int m = min(mb + r0 + RRPP * p, a.M - 1);
-                tix[p] = ada_row(a.ada, m);
-            }
 #pragma unroll
             for (int p = 0; p < RNP; p++) {
                 const int m = min(mb + r0 + RRPP * p, a.M - 1);
                 rs[p] = *(const f32x4*)(a.resid + (size_t)m * a.ldo + n);
-                gt[p] = *(const f32x4*)(a.ada.tstab + ((size_t)tix[p] * 9 + a.igate) * LTX_D + n);
+                gt[p] = *(const f32x4*)(a.ada.tstab + ((size_t)tixn[p] * 9 + a.igate) * LTX_D + n);
             }
+            if (i + 1 < NI)
+#pragma unroll
+                for (int p = 0; p < RNP; p++) tixn[p] = ada_row(a.ada, min(mb + 32 + r0 + RRPP * p, a.M - 1));
         }
 #pragma unroll
         for (int j = 0; j < NJ; j++)
