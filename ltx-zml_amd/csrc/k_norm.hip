@@ -138,7 +138,8 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* out) {
 template <typename T>
 __device__ void qknorm_body(const LtxQkNormArgs& a) {
     __shared__ float red[4];
-    int row = blockIdx.x;
+    // a contiguous range of tokens per XCD, as in qknorm2_body
+    const int row = (gridDim.x & 7) == 0 ? (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3) : blockIdx.x;
     if (row >= a.rows) return;
     int h = threadIdx.x >> 3, f0 = (threadIdx.x & 7) * 8;
     const uint16_t* xr = (const uint16_t*)a.x + (size_t)row * a.ldx + h * LTX_HD;
@@ -202,7 +203,11 @@ __device__ void qknorm_body(const LtxQkNormArgs& a) {
 template <typename T>
 __device__ void qknorm2_body(const LtxQkNorm2Args& a) {
     __shared__ float red[8];
-    const int row = blockIdx.x;
+    // workgroups go round-robin to the 8 XCDs: give each XCD a contiguous
+    // range of tokens, so that its L2 sees whole runs of consecutive rows of
+    // every head-major output (measured: qknorm2 -1.5 %, and the gate logits
+    // beside it on the side stream 0.245 -> 0.170 ms)
+    const int row = (gridDim.x & 7) == 0 ? (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3) : blockIdx.x;
     if (row >= a.rows) return;
     const int h = threadIdx.x >> 3, f0 = (threadIdx.x & 7) * 8;
     float lo[2][8], hi[2][8], cs[8], sn[8], wlo[2][8], whi[2][8];
