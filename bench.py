@@ -460,8 +460,6 @@ def main() -> int:
     torch.cuda.synchronize()
     assert torch.isfinite(y).all().item(), "non-finite block output"
     log("bench: warmup done")
-    ctx.profile(True)
-    ctx.profile_reset()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(stream)
@@ -470,10 +468,15 @@ def main() -> int:
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
-    per = {}
-    for lab in KERNEL_LABELS:
-        tot, n = ctx.profile_read(lab)
-        per[lab] = round(tot / max(n, 1), 4)
+    # per-kernel times of the same forward in a separate pass (the events
+    # around each launch stay out of the timed region): per forward, summed
+    # over a label's launches
+    ctx.profile(True)
+    ctx.profile_reset()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    per = {lab: round(ctx.profile_read(lab)[0] / args.steps, 4) for lab in KERNEL_LABELS}
     ctx.profile(False)
     f = flops(T, S)
     total = sum(f.values())

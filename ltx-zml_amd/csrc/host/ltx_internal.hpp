@@ -87,6 +87,10 @@ struct ltx_ctx {
     // cross-attention K/V) overlaps it, ordered by the events
     hipStream_t side = nullptr;
     hipEvent_t side_ev[4] = {};
+    // markers recorded after every launch outside profiling mode (no timing,
+    // no system-scope fence), cycled
+    hipEvent_t marks[16] = {};
+    unsigned mark_i = 0;
     std::vector<hipModule_t> modules;
     std::map<std::string, hipFunction_t> fns;
     std::string err;
