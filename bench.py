@@ -32,7 +32,7 @@ PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
 # FETCH_SIZE x 2.0 (the factor a 1 GiB copy calibrates) + WRITE_SIZE x 1.0,
 # measured on this kernel (profiles/block_t28672_hbm_bytes.md); None for a
 # size or type not profiled.
-ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.468e9, (28672, "bf16"): 2.467e9}
+ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.470e9, (28672, "bf16"): 2.468e9}
 
 
 def flops(T: int, S: int) -> dict:
