@@ -334,6 +334,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     if (T <= 0 || S <= 0 || K <= 0) throw Error("T, S and K must be positive");
     if (!x || !tstab || !tidx || !ctxv || !pts2 || !cs || !sn || !y) throw Error("NULL tensor argument");
     if ((const void*)x == (const void*)y) throw Error("y may not alias x");
+    MarkScope marks(c, T >= kMarkRows);
     if (mode != LTX_MODE_F16 && mode != LTX_MODE_BF16 && mode != LTX_MODE_F32) throw Error("unknown mode");
     HIPC(hipSetDevice(c->device));
     ensure_ws(c, (size_t)T, (size_t)S, mode);
@@ -582,6 +583,7 @@ int ltx_op_linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* sca
             sc.q = (uint32_t*)c->op_q.p;
             sc.pairs = (uint32_t*)c->op_pairs.p;
         }
+        ltx::MarkScope marks(c, M >= ltx::kMarkRows);
         ltx::linear_q8(c, a, q, scales, scale_f16, bias, y, out_f32, M, N, K, gelu, mode, sc, (hipStream_t)stream);
     })
 }
@@ -595,6 +597,7 @@ int ltx_op_attention(ltx_ctx* c, const void* q, const void* k, const void* v, co
         mode &= ~LTX_ATTN_Q_SCALED;
         if (q_scaled && mode == LTX_MODE_F32) throw ltx::Error("LTX_ATTN_Q_SCALED applies to the 16-bit modes");
         HIPC(hipSetDevice(c->device));
+        ltx::MarkScope marks(c, lq >= ltx::kMarkRows);
         if (mode == LTX_MODE_F32)
             ltx::attn32(c, (const float*)q, (const float*)k, (const float*)v, glog, (float*)out, lq, lkv,
                         (hipStream_t)stream);

@@ -87,10 +87,11 @@ struct ltx_ctx {
     // cross-attention K/V) overlaps it, ordered by the events
     hipStream_t side = nullptr;
     hipEvent_t side_ev[4] = {};
-    // markers recorded after every launch outside profiling mode (no timing,
-    // no system-scope fence), cycled
+    // markers recorded after each launch of a call with long kernels (see
+    // launch), cycled; no timing, no system-scope fence
     hipEvent_t marks[16] = {};
     unsigned mark_i = 0;
+    bool marks_on = false;
     std::vector<hipModule_t> modules;
     std::map<std::string, hipFunction_t> fns;
     std::string err;
@@ -118,6 +119,18 @@ struct ltx_ctx {
 };
 
 namespace ltx {
+// Markers after each launch for the duration of one call whose kernels are
+// long: the block forward and the isolated ops from 8,192 rows up.
+struct MarkScope {
+    ltx_ctx* c;
+    bool prev;
+    MarkScope(ltx_ctx* ctx, bool on) : c(ctx), prev(ctx->marks_on) { c->marks_on = on; }
+    ~MarkScope() { c->marks_on = prev; }
+    MarkScope(const MarkScope&) = delete;
+    MarkScope& operator=(const MarkScope&) = delete;
+};
+constexpr int kMarkRows = 8192;
+
 void set_thread_error(const std::string& e);
 void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const float* tstab, int K,
                    const int32_t* tidx, const float* ctxv, int S, const float* pts2, const float* cs,

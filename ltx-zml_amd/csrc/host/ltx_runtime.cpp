@@ -123,12 +123,14 @@ void ltx_ctx::launch(const char* name, unsigned gx, unsigned gy, unsigned gz, un
     if (prof) {
         HIPC(hipEventRecord(eb, st));
         prof_recs.push_back({label ? label : fns.find(name)->first.c_str(), ea, eb});
-    } else {
-        // A marker after each kernel. Measured on six boxes: the 28,672-token
-        // block took 1.5-1.9 % less time on five (22.8-23.2 -> 22.4-22.9 ms)
-        // and the same on the sixth, whether the marker carried a timing
-        // stamp, a system-scope fence or neither; markers on the second
-        // stream alone did nothing. The runtime's handling of back-to-back
+    } else if (marks_on) {
+        // A marker after each kernel of a call with long kernels. Measured
+        // on seven boxes: the 28,672-token block took 1-1.9 % less time on
+        // six (22.8-23.4 -> 22.4-23.2 ms) and the same on the seventh,
+        // whether the marker carried a timing stamp, a system-scope fence or
+        // neither; markers on the second stream alone did nothing. The
+        // 1,024-token block (kernels of 4-130 us) took 2 % more, hence the
+        // size switch (MarkScope). The runtime's handling of back-to-back
         // dispatches without one is the suspected cause; not identified.
         HIPC(hipEventRecord(marks[mark_i++ & 15], st));
     }
