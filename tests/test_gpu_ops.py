@@ -203,7 +203,9 @@ def _heads(x, L):  # [L, D] -> [H, L, 128]
                                           (100, 128, True), (300, 160, True), (256, 480, False),
                                           # resident K/V (64-256 keys): several query tiles per workgroup,
                                           # a ragged last tile, one to four key tiles
-                                          (4000, 256, True), (3000, 64, True), (2100, 192, False)])
+                                          (4000, 256, True), (3000, 64, True), (2100, 192, False),
+                                          # one key tile and a single ragged query tile per head
+                                          (200, 64, True)])
 @pytest.mark.parametrize("q_scaled", [False, True])
 def test_attention(ctx, mode, lq, lkv, gated, q_scaled):
     """q_scaled: q arrives multiplied by log2(e)/sqrt(128), as the block's
