@@ -685,17 +685,6 @@ struct AttnPP {
         range_report(a.sat, bad);
     }
 
-    // Resident K/V (lkv = 64 nt, 1 <= nt <= 4): the workgroup loads head h's
-    // whole K and V^T into LDS once (kres, vres: nt tiles of 16 KB each, the
-    // stage layouts above), then runs query tiles qt0, qt0 + wph, ... of that
-    // head with no DMA, as one continuous ping-pong over the (query tile, key
-    // tile) sequence: the MFMA phase after the last softmax of tile i runs
-    // PV_i(nt - 1) and S_i+1(0), and tile i's output is stored in the next
-    // softmax phase, before softmax_i+1(0) clears O and l. The running max
-    // and the Q^T operands switch to tile i + 1 at the end of softmax_i(nt -
-    // 1). The next tile's Q and the tile's gate logits load while it runs.
-    // Every query tile takes 2 nt barriers in both groups (group 1 keeps its
-    // one-phase lag), plus one after the final PV.
     // the softmax phase's results stay in registers (not rematerialised in
     // the next phase)
     __device__ __forceinline__ void pin_softmax() {
@@ -726,6 +715,17 @@ struct AttnPP {
         barrier();
     }
 
+    // Resident K/V (lkv = 64 nt, 1 <= nt <= 4): the workgroup loads head h's
+    // whole K and V^T into LDS once (kres, vres: nt tiles of 16 KB each, the
+    // stage layouts above), then runs query tiles qt0, qt0 + wph, ... of that
+    // head with no DMA, as one continuous ping-pong over the (query tile, key
+    // tile) sequence: the MFMA phase after the last softmax of tile i runs
+    // PV_i(nt - 1) and S_i+1(0), and tile i's output is stored in the next
+    // softmax phase, before softmax_i+1(0) clears O and l. The running max
+    // and the Q^T operands switch to tile i + 1 at the end of softmax_i(nt -
+    // 1). The next tile's Q and the tile's gate logits load while it runs.
+    // Every query tile takes 2 nt barriers in both groups (group 1 keeps its
+    // one-phase lag), plus one after the final PV.
     __device__ __forceinline__ void run_resident(uint8_t* kres, uint8_t* vres, uint16_t* patches) {
         const int tid = threadIdx.x, lane = tid & 63;
         const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
