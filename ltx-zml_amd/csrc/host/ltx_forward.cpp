@@ -334,7 +334,6 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     if (T <= 0 || S <= 0 || K <= 0) throw Error("T, S and K must be positive");
     if (!x || !tstab || !tidx || !ctxv || !pts2 || !cs || !sn || !y) throw Error("NULL tensor argument");
     if ((const void*)x == (const void*)y) throw Error("y may not alias x");
-    MarkScope marks(c, T >= kMarkRows);
     if (mode != LTX_MODE_F16 && mode != LTX_MODE_BF16 && mode != LTX_MODE_F32) throw Error("unknown mode");
     HIPC(hipSetDevice(c->device));
     ensure_ws(c, (size_t)T, (size_t)S, mode);
@@ -437,23 +436,30 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.sat = sat;
     g.part = (float*)b.part;  // split-K partial sums (small grids)
     gemm16(c, mode, w->q2, b.attn_in, T, LTX_D, LTX_EPI_STORE, g, st, "gemm:q2");
-    // the cross-attention gate logits on the side stream, beside the context
-    // side (K/V modulation, k|v GEMM) and the q and k norms
-    stream_after(sd, st, c->side_ev[2]);
-    gate16(c, mode, w->g2, b.attn_in, T, (float*)b.glog2, sd);
-    LtxEncArgs ea{ctxv, (const float*)w->psst.p, pts2, b.enc, S, sat};
-    c->launch(mode == LTX_MODE_BF16 ? "ltx_enc_bf16" : "ltx_enc_f16", S, 1, 1, 256, &ea, st);
-    g = LtxGemmArgs{};
-    g.out = b.k2_16;
-    g.out2 = b.vt2;
-    g.nsplit = LTX_D;
-    g.sat = sat;
-    g.part = (float*)b.part;  // split-K partial sums (small grids)
-    gemm16(c, mode, w->kv2, b.enc, S, LTX_D, LTX_EPI_QKV, g, st, "gemm:kv2");
-    qknorm16(c, mode, b.q2_16, LTX_D, w->qn2.p, nullptr, nullptr, b.qh2, T, kAttnC, st);
-    qknorm16(c, mode, b.k2_16, LTX_D, w->kn2.p, nullptr, nullptr, b.kh2, S, 1.0f, st);
-    stream_after(st, sd, c->side_ev[3]);  // glog2 ready
-    attn16(c, mode, b.qh2, b.kh2, b.vt2, (const float*)b.glog2, b.o2, T, S, true, st, "attn:cross", sat);
+    {
+        // A marker after each launch from here to the cross-attention (see
+        // ltx_ctx::launch): without them the gate logits below and the k|v
+        // GEMM's split-K reduce beside them interleaved so badly that they
+        // took 0.57 and 0.39 ms instead of 0.09 and 0.01 (28,672 tokens).
+        MarkScope marks(c, T >= kMarkRows);
+        // the cross-attention gate logits on the side stream, beside the
+        // context side (K/V modulation, k|v GEMM) and the q and k norms
+        stream_after(sd, st, c->side_ev[2]);
+        gate16(c, mode, w->g2, b.attn_in, T, (float*)b.glog2, sd);
+        LtxEncArgs ea{ctxv, (const float*)w->psst.p, pts2, b.enc, S, sat};
+        c->launch(mode == LTX_MODE_BF16 ? "ltx_enc_bf16" : "ltx_enc_f16", S, 1, 1, 256, &ea, st);
+        g = LtxGemmArgs{};
+        g.out = b.k2_16;
+        g.out2 = b.vt2;
+        g.nsplit = LTX_D;
+        g.sat = sat;
+        g.part = (float*)b.part;  // split-K partial sums (small grids)
+        gemm16(c, mode, w->kv2, b.enc, S, LTX_D, LTX_EPI_QKV, g, st, "gemm:kv2");
+        qknorm16(c, mode, b.q2_16, LTX_D, w->qn2.p, nullptr, nullptr, b.qh2, T, kAttnC, st);
+        qknorm16(c, mode, b.k2_16, LTX_D, w->kn2.p, nullptr, nullptr, b.kh2, S, 1.0f, st);
+        stream_after(st, sd, c->side_ev[3]);  // glog2 ready
+        attn16(c, mode, b.qh2, b.kh2, b.vt2, (const float*)b.glog2, b.o2, T, S, true, st, "attn:cross", sat);
+    }
     g = LtxGemmArgs{};
     g.out = b.x_ca;
     g.resid = (const float*)b.x_sa;
@@ -583,7 +589,6 @@ int ltx_op_linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* sca
             sc.q = (uint32_t*)c->op_q.p;
             sc.pairs = (uint32_t*)c->op_pairs.p;
         }
-        ltx::MarkScope marks(c, M >= ltx::kMarkRows);
         ltx::linear_q8(c, a, q, scales, scale_f16, bias, y, out_f32, M, N, K, gelu, mode, sc, (hipStream_t)stream);
     })
 }
@@ -597,7 +602,6 @@ int ltx_op_attention(ltx_ctx* c, const void* q, const void* k, const void* v, co
         mode &= ~LTX_ATTN_Q_SCALED;
         if (q_scaled && mode == LTX_MODE_F32) throw ltx::Error("LTX_ATTN_Q_SCALED applies to the 16-bit modes");
         HIPC(hipSetDevice(c->device));
-        ltx::MarkScope marks(c, lq >= ltx::kMarkRows);
         if (mode == LTX_MODE_F32)
             ltx::attn32(c, (const float*)q, (const float*)k, (const float*)v, glog, (float*)out, lq, lkv,
                         (hipStream_t)stream);

@@ -87,8 +87,8 @@ struct ltx_ctx {
     // cross-attention K/V) overlaps it, ordered by the events
     hipStream_t side = nullptr;
     hipEvent_t side_ev[4] = {};
-    // markers recorded after each launch of a call with long kernels (see
-    // launch), cycled; no timing, no system-scope fence
+    // markers recorded after each launch inside a MarkScope (see launch),
+    // cycled; no timing, no system-scope fence
     hipEvent_t marks[16] = {};
     unsigned mark_i = 0;
     bool marks_on = false;
@@ -119,8 +119,9 @@ struct ltx_ctx {
 };
 
 namespace ltx {
-// Markers after each launch for the duration of one call whose kernels are
-// long: the block forward and the isolated ops from 8,192 rows up.
+// Markers after each launch for the duration of a scope: the stretch of a
+// block forward (from 8,192 tokens) in which the second stream's gate logits
+// run beside the context k|v GEMM (ltx_ctx::launch).
 struct MarkScope {
     ltx_ctx* c;
     bool prev;

@@ -124,17 +124,18 @@ void ltx_ctx::launch(const char* name, unsigned gx, unsigned gy, unsigned gz, un
         HIPC(hipEventRecord(eb, st));
         prof_recs.push_back({label ? label : fns.find(name)->first.c_str(), ea, eb});
     } else if (marks_on) {
-        // A marker after each kernel of a call with long kernels. Without
-        // them (kernel traces of the 28,672-token block) the cross-attention
-        // gate logits on the second stream and the context k|v GEMM's
-        // split-K reduce beside them took 0.568 and 0.394 ms instead of
-        // 0.089 and 0.014 ms; every other kernel ran within 1 %. The block
-        // took 1-2.3 % less time with the markers on six of seven boxes,
-        // whether they carried a timing stamp, a system-scope fence or
-        // neither; markers on the second stream alone, or one marker just
-        // before or after the reduce, did not help. The 1,024-token block
-        // (kernels of 4-130 us) took 2 % more, hence the size switch
-        // (MarkScope).
+        // A marker after each kernel inside a MarkScope: the stretch of the
+        // block forward from the q2 GEMM to the cross-attention. Without them
+        // (kernel traces of the 28,672-token block) the cross-attention gate
+        // logits on the second stream and the context k|v GEMM's split-K
+        // reduce beside them took 0.568 and 0.394 ms instead of 0.089 and
+        // 0.014 ms; every other kernel ran within 1 %. The block took
+        // 1-2.3 % less time with markers on six of seven boxes, whether they
+        // carried a timing stamp, a system-scope fence or neither; markers on
+        // the second stream alone, or one marker just before or after the
+        // reduce, did not help, and markers on every launch of the forward
+        // helped no more than on this stretch. At 1,024 tokens (kernels of
+        // 4-130 us) markers on every launch cost 2 %, hence the size switch.
         HIPC(hipEventRecord(marks[mark_i++ & 15], st));
     }
 }
