@@ -19,10 +19,11 @@ next T/7, 1 for the rest — K = 3 distinct rows gathered through tidx.
 from __future__ import annotations
 
 import zlib
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
-from .blockfmt import D, bf16_bits, bf16_to_f32
+from .blockfmt import D
 
 TE, HALF = 256, 128
 
@@ -31,12 +32,44 @@ def _rng(seed: int, name: str) -> np.random.Generator:
     return np.random.default_rng([seed, zlib.crc32(name.encode())])
 
 
+_CHUNK = 1 << 20
+
+
+def _draw_bf16(seed: int, name: str, shape) -> np.ndarray:
+    """N(0, 1) * 0.02 rounded to bf16 (nearest even), as f32 values.
+
+    Drawn and rounded in chunks in place: the generator's stream does not
+    depend on how the draws are split, and the values are finite, so this
+    equals bf16_to_f32(bf16_bits(standard_normal(shape) * 0.02))."""
+    g = _rng(seed, name)
+    out = np.empty(int(np.prod(shape)), dtype=np.float32)
+    u = out.view(np.uint32)
+    for i in range(0, out.size, _CHUNK):
+        c = out[i:i + _CHUNK]
+        g.standard_normal(out=c, dtype=np.float32)
+        c *= np.float32(0.02)
+        cu = u[i:i + _CHUNK]
+        r = (cu >> 16) & np.uint32(1)
+        r += np.uint32(0x7FFF)
+        cu += r
+        cu &= np.uint32(0xFFFF0000)
+    return out.reshape(shape)
+
+
 def _bits(seed: int, name: str, shape) -> np.ndarray:
-    return bf16_bits(_rng(seed, name).standard_normal(shape, dtype=np.float32) * 0.02)
+    return (_draw_bf16(seed, name, shape).view(np.uint32) >> 16).astype(np.uint16)
 
 
 def _w(seed: int, name: str, shape) -> np.ndarray:
-    return bf16_to_f32(_bits(seed, name, shape))
+    return _draw_bf16(seed, name, shape)
+
+
+def _parallel(fn, jobs):
+    """{name: fn(seed, name, shape)} for jobs [(seed, name, shape)], the
+    tensors drawn on worker threads (each has its own generator)."""
+    with ThreadPoolExecutor(max_workers=8) as ex:
+        futs = {j[1]: ex.submit(fn, *j) for j in jobs}
+        return {k: f.result() for k, f in futs.items()}
 
 
 # The core tensors in CORE_SPECS order (ltx/core_parts.zig:53-72): name,
@@ -57,13 +90,14 @@ def make_core(seed: int = 7) -> dict:
     """Seeded core tensors: bf16 bits (uint16) ~ N(0, 0.02) for the linear
     layers, the same draws ``tables`` uses for the conditioning MLPs; fsst
     f32 ~ N(0, 1) / sqrt(D)."""
+    bits = _parallel(_bits, [(seed, name, shape) for name, shape in CORE_SPECS if name != "fsst"])
     out = {}
     for name, shape in CORE_SPECS:
         if name == "fsst":
             g = _rng(seed, name)
             out[name] = (g.standard_normal(shape, dtype=np.float32) / np.float32(np.sqrt(D))).astype(np.float32)
         else:
-            out[name] = _bits(seed, name, shape)
+            out[name] = bits[name]
     return out
 
 
@@ -96,17 +130,13 @@ def _silu(x):
 
 
 def _mlp_tables(seed: int):
-    w = {}
+    jobs = []
     for pfx in ("ada", "pada"):
-        w[pfx + "_l1_w"] = _w(seed, pfx + "_l1_w", (D, TE))
-        w[pfx + "_l1_b"] = _w(seed, pfx + "_l1_b", (D,))
-        w[pfx + "_l2_w"] = _w(seed, pfx + "_l2_w", (D, D))
-        w[pfx + "_l2_b"] = _w(seed, pfx + "_l2_b", (D,))
-    w["ada_out_w"] = _w(seed, "ada_out_w", (9 * D, D))
-    w["ada_out_b"] = _w(seed, "ada_out_b", (9 * D,))
-    w["pada_out_w"] = _w(seed, "pada_out_w", (2 * D, D))
-    w["pada_out_b"] = _w(seed, "pada_out_b", (2 * D,))
-    return w
+        jobs += [(seed, pfx + "_l1_w", (D, TE)), (seed, pfx + "_l1_b", (D,)),
+                 (seed, pfx + "_l2_w", (D, D)), (seed, pfx + "_l2_b", (D,))]
+    jobs += [(seed, "ada_out_w", (9 * D, D)), (seed, "ada_out_b", (9 * D,)),
+             (seed, "pada_out_w", (2 * D, D)), (seed, "pada_out_b", (2 * D,))]
+    return _parallel(_w, jobs)
 
 
 _CACHE: dict = {}
