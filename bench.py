@@ -28,6 +28,7 @@ sys.path.insert(0, str(ROOT))
 
 D, H, HD, FF = 4096, 32, 128, 16384
 PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
+PEAK_F32_TFLOPS = 157.3  # MI355X fp32 (the f32 mode's kernels are SIMT f32)
 # HBM bytes per self-attention launch, by (tokens, operand type): rocprofv3
 # FETCH_SIZE x 2.0 (the factor a 1 GiB copy calibrates) + WRITE_SIZE x 1.0,
 # measured on this kernel (profiles/block_t28672_hbm_bytes.md); None for a
@@ -386,7 +387,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--mode", default="f16", choices=["f16", "bf16"])
+    ap.add_argument("--mode", default="f16", choices=["f16", "bf16", "f32"],
+                    help="operand type of the block bench (f32: the exact SIMT path, no denoise leg)")
     ap.add_argument("--tokens", type=int, default=28672)
     ap.add_argument("--text", type=int, default=256)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -429,6 +431,8 @@ def main() -> int:
     if args.denoise:
         return denoise_bench(args)
     if args.sweep:
+        if args.mode == "f32":
+            sys.exit("bench: --sweep times the 16-bit kernels (--mode f16 or bf16)")
         return sweep_bench(args)
     t0 = time.time()
     bt = synth.make_block(0, seed=1, dist="t3", classes=("qkv", "ff", "out") if args.weights == "int8" else (),
@@ -482,6 +486,7 @@ def main() -> int:
     ctx.profile(False)
     f = flops(T, S)
     total = sum(f.values())
+    peak = PEAK_F32_TFLOPS if args.mode == "f32" else PEAK_TFLOPS
     attn_ms = per["attn:self"]
     achieved = f["self_attn"] / (attn_ms * 1e-3) / 1e12
     gemm_ms = sum(v for k, v in per.items() if k.startswith("gemm:"))
@@ -493,7 +498,7 @@ def main() -> int:
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f16" if args.mode == "f16" else "bf16",
+        "dtype": args.mode,
         "weights": ("int8 grouped-128, " + ("fp16" if args.scales == "f16" else "f32") + " scales")
                    if args.weights == "int8" else "bf16 (unquantised)",
         "data": "synthetic",
@@ -509,12 +514,13 @@ def main() -> int:
         # included): the MFMA kernels' share of the peak
         "gemm_attn_pct_peak": round(100.0 * (total - 4 * T * D * H)
                                     / ((gemm_ms + per["splitk_reduce"] + attn_ms + per["attn:cross"]) * 1e-3)
-                                    / 1e12 / PEAK_TFLOPS, 2),
+                                    / 1e12 / peak, 2),
         "kernel_ms": per,
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_TFLOPS, 4),
+        "roofline": {"bound": "mfma" if args.mode != "f32" else "valu", "achieved": round(achieved, 1), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                      "traffic": ATTN_SELF_TRAFFIC.get((T, args.mode)),
-                     "kernel": "ltx_attn_" + args.mode + "_pp (self-attention, 4*H*T^2*HD = "
+                     "kernel": "ltx_attn_" + args.mode + ("_pp" if args.mode != "f32" else "")
+                               + " (self-attention, 4*H*T^2*HD = "
                                f"{f['self_attn'] / 1e12:.3f} TFLOP per launch)"},
     }
     w.free()
@@ -550,7 +556,9 @@ def main() -> int:
     ctx.profile(False)
     log(f"bench: T=1024 block {res['t1024_block_ms']:.3f} ms")
     w0.free()
-    if not args.no_denoise:
+    if args.mode == "f32":
+        log("bench: no denoise leg in f32 mode")
+    elif not args.no_denoise:
         # the full-transformer loop: 48 resident int8 blocks x 8 stage-1 steps
         # at the same 28,672 tokens (after the timed block region)
         res["denoise"] = denoise_steps(ctx, bt, T, S, 48, mode)

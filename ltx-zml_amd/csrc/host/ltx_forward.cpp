@@ -276,7 +276,8 @@ static void attn16(ltx_ctx* c, int mode, const void* q, const void* k, const voi
 
 // f32-mode GEMM over rows [r0, r0 + N) of a (possibly fused) projection.
 static void gemm32(ltx_ctx* c, const LtxProj& p, int r0, int N, const float* A, int M, float* out, int epi,
-                   const float* resid, LtxAda ada, int igate, int gelu, hipStream_t st) {
+                   const float* resid, LtxAda ada, int igate, int gelu, hipStream_t st,
+                   const char* label = nullptr) {
     LtxGemm32Args g{};
     g.a = A;
     const size_t G = p.K / LTX_GROUP;
@@ -299,7 +300,7 @@ static void gemm32(ltx_ctx* c, const LtxProj& p, int r0, int N, const float* A, 
     g.epi = epi;
     g.gelu = gelu;
     g.igate = igate;
-    c->launch("ltx_gemm_f32", (N + 63) / 64, (M + 63) / 64, 1, 256, &g, st);
+    c->launch("ltx_gemm_f32", (N + 63) / 64, (M + 63) / 64, 1, 256, &g, st, label);
 }
 
 static void qknorm32(ltx_ctx* c, float* x, const void* w, const float* cs, const float* sn, int rows, hipStream_t st) {
@@ -308,9 +309,9 @@ static void qknorm32(ltx_ctx* c, float* x, const void* w, const float* cs, const
 }
 
 static void attn32(ltx_ctx* c, const float* q, const float* k, const float* v, const float* glog, float* out, int lq,
-                   int lkv, hipStream_t st) {
+                   int lkv, hipStream_t st, const char* label = nullptr) {
     LtxAttn32Args a{q, k, v, glog, out, lq, lkv, 1.0f / std::sqrt(128.0f)};
-    c->launch("ltx_attn_f32", (lq + 63) / 64, LTX_H, 1, 64, &a, st);
+    c->launch("ltx_attn_f32", (lq + 63) / 64, LTX_H, 1, 64, &a, st, label);
 }
 
 // `to` runs what it is given next only after everything enqueued so far on
@@ -347,30 +348,30 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
         carve32(cv, b, T, S);
         // self-attention (ltx/block.zig:546-547, qAttn1 520-530)
         norm_mod(c, mode, x, b.n_msa, ada, T, 0, 1, st);
-        gemm32(c, w->qkv1, 0, LTX_D, (const float*)b.n_msa, T, (float*)b.q, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
-        gemm32(c, w->qkv1, LTX_D, LTX_D, (const float*)b.n_msa, T, (float*)b.k, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
-        gemm32(c, w->qkv1, 2 * LTX_D, LTX_D, (const float*)b.n_msa, T, (float*)b.v, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
-        gemm32(c, w->g1, 0, LTX_H, (const float*)b.n_msa, T, (float*)b.glog1, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
+        gemm32(c, w->qkv1, 0, LTX_D, (const float*)b.n_msa, T, (float*)b.q, LTX_EPI_STORE, nullptr, ada, 0, 0, st, "gemm:qkv1");
+        gemm32(c, w->qkv1, LTX_D, LTX_D, (const float*)b.n_msa, T, (float*)b.k, LTX_EPI_STORE, nullptr, ada, 0, 0, st, "gemm:qkv1");
+        gemm32(c, w->qkv1, 2 * LTX_D, LTX_D, (const float*)b.n_msa, T, (float*)b.v, LTX_EPI_STORE, nullptr, ada, 0, 0, st, "gemm:qkv1");
+        gemm32(c, w->g1, 0, LTX_H, (const float*)b.n_msa, T, (float*)b.glog1, LTX_EPI_STORE, nullptr, ada, 0, 0, st, "ltx_gate:1");
         qknorm32(c, (float*)b.q, w->qn1.p, cs, sn, T, st);
         qknorm32(c, (float*)b.k, w->kn1.p, cs, sn, T, st);
-        attn32(c, (const float*)b.q, (const float*)b.k, (const float*)b.v, (const float*)b.glog1, (float*)b.o1, T, T, st);
-        gemm32(c, w->o1, 0, LTX_D, (const float*)b.o1, T, (float*)b.x_sa, LTX_EPI_RESID_GATE, x, ada, 2, 0, st);
+        attn32(c, (const float*)b.q, (const float*)b.k, (const float*)b.v, (const float*)b.glog1, (float*)b.o1, T, T, st, "attn:self");
+        gemm32(c, w->o1, 0, LTX_D, (const float*)b.o1, T, (float*)b.x_sa, LTX_EPI_RESID_GATE, x, ada, 2, 0, st, "gemm:o1");
         // cross-attention (ltx/block.zig:548-568)
         norm_mod(c, mode, (const float*)b.x_sa, b.attn_in, ada, T, 6, 7, st);
         LtxEncArgs ea{ctxv, (const float*)w->psst.p, pts2, b.enc, S};
         c->launch("ltx_enc_f32", S, 1, 1, 256, &ea, st);
-        gemm32(c, w->q2, 0, LTX_D, (const float*)b.attn_in, T, (float*)b.q2, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
-        gemm32(c, w->kv2, 0, LTX_D, (const float*)b.enc, S, (float*)b.k2, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
-        gemm32(c, w->kv2, LTX_D, LTX_D, (const float*)b.enc, S, (float*)b.v2, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
-        gemm32(c, w->g2, 0, LTX_H, (const float*)b.attn_in, T, (float*)b.glog2, LTX_EPI_STORE, nullptr, ada, 0, 0, st);
+        gemm32(c, w->q2, 0, LTX_D, (const float*)b.attn_in, T, (float*)b.q2, LTX_EPI_STORE, nullptr, ada, 0, 0, st, "gemm:q2");
+        gemm32(c, w->kv2, 0, LTX_D, (const float*)b.enc, S, (float*)b.k2, LTX_EPI_STORE, nullptr, ada, 0, 0, st, "gemm:kv2");
+        gemm32(c, w->kv2, LTX_D, LTX_D, (const float*)b.enc, S, (float*)b.v2, LTX_EPI_STORE, nullptr, ada, 0, 0, st, "gemm:kv2");
+        gemm32(c, w->g2, 0, LTX_H, (const float*)b.attn_in, T, (float*)b.glog2, LTX_EPI_STORE, nullptr, ada, 0, 0, st, "ltx_gate:2");
         qknorm32(c, (float*)b.q2, w->qn2.p, nullptr, nullptr, T, st);
         qknorm32(c, (float*)b.k2, w->kn2.p, nullptr, nullptr, S, st);
-        attn32(c, (const float*)b.q2, (const float*)b.k2, (const float*)b.v2, (const float*)b.glog2, (float*)b.o2, T, S, st);
-        gemm32(c, w->o2, 0, LTX_D, (const float*)b.o2, T, (float*)b.x_ca, LTX_EPI_RESID_GATE, (const float*)b.x_sa, ada, 8, 0, st);
+        attn32(c, (const float*)b.q2, (const float*)b.k2, (const float*)b.v2, (const float*)b.glog2, (float*)b.o2, T, S, st, "attn:cross");
+        gemm32(c, w->o2, 0, LTX_D, (const float*)b.o2, T, (float*)b.x_ca, LTX_EPI_RESID_GATE, (const float*)b.x_sa, ada, 8, 0, st, "gemm:o2");
         // feed-forward (ltx/block.zig:569-573)
         norm_mod(c, mode, (const float*)b.x_ca, b.ff_in, ada, T, 3, 4, st);
-        gemm32(c, w->f1, 0, LTX_FF, (const float*)b.ff_in, T, (float*)b.h, LTX_EPI_STORE, nullptr, ada, 0, 1, st);
-        gemm32(c, w->f2, 0, LTX_D, (const float*)b.h, T, y, LTX_EPI_RESID_GATE, (const float*)b.x_ca, ada, 5, 0, st);
+        gemm32(c, w->f1, 0, LTX_FF, (const float*)b.ff_in, T, (float*)b.h, LTX_EPI_STORE, nullptr, ada, 0, 1, st, "gemm:ff1");
+        gemm32(c, w->f2, 0, LTX_D, (const float*)b.h, T, y, LTX_EPI_RESID_GATE, (const float*)b.x_ca, ada, 5, 0, st, "gemm:ff2");
         set_stage(c, LTX_ST_NORM_MSA, b.n_msa, TD * 4);
         set_stage(c, LTX_ST_Q1, b.q, TD * 4);
         set_stage(c, LTX_ST_K1, b.k, TD * 4);
