@@ -311,7 +311,7 @@ static void qknorm32(ltx_ctx* c, float* x, const void* w, const float* cs, const
 static void attn32(ltx_ctx* c, const float* q, const float* k, const float* v, const float* glog, float* out, int lq,
                    int lkv, hipStream_t st, const char* label = nullptr) {
     LtxAttn32Args a{q, k, v, glog, out, lq, lkv, 1.0f / std::sqrt(128.0f)};
-    c->launch("ltx_attn_f32", (lq + 63) / 64, LTX_H, 1, 64, &a, st, label);
+    c->launch("ltx_attn_f32", (lq + 127) / 128, LTX_H, 1, 512, &a, st, label);
 }
 
 // `to` runs what it is given next only after everything enqueued so far on

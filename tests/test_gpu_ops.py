@@ -235,10 +235,10 @@ def test_attention(ctx, mode, lq, lkv, gated, q_scaled):
     assert oracle.rel_rms(f64(out), want) <= (2e-3 if mode == "f16" else 1e-2)
 
 
-def test_attention_f32_mode(ctx):
-    say("attention mode=f32 lq=130 lkv=70")
-    rng = np.random.default_rng(11)
-    lq, lkv = 130, 70
+@pytest.mark.parametrize("lq,lkv", [(130, 70), (1000, 1000), (257, 193), (64, 1)])
+def test_attention_f32_mode(ctx, lq, lkv):
+    say(f"attention mode=f32 lq={lq} lkv={lkv}")
+    rng = np.random.default_rng(11 + lq + lkv)
     q, k, v = (rng.standard_normal((n, 4096)).astype(np.float32) for n in (lq, lkv, lkv))
     glog = rng.standard_normal((lq, 32)).astype(np.float32)
     out = torch.empty((lq, 4096), dtype=torch.float32, device="cuda")
