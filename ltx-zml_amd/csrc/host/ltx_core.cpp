@@ -52,7 +52,8 @@ static void lin32(ltx_ctx* c, const ltx_core_weights* cw, int wi, const float* A
     g.N = s.o;
     g.K = s.i;
     g.epi = LTX_EPI_STORE;
-    c->launch("ltx_gemm_f32", (s.o + 63) / 64, (M + 63) / 64, 1, 256, &g, st);
+    if (s.i % 32) throw Error("core GEMM: K must be a multiple of 32");
+    c->launch("ltx_gemm_f32", (s.o + 127) / 128, (M + 127) / 128, 1, 256, &g, st);
 }
 
 static void silu(ltx_ctx* c, const float* x, float* y, size_t n, hipStream_t st) {

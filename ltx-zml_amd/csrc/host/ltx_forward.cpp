@@ -300,7 +300,8 @@ static void gemm32(ltx_ctx* c, const LtxProj& p, int r0, int N, const float* A, 
     g.epi = epi;
     g.gelu = gelu;
     g.igate = igate;
-    c->launch("ltx_gemm_f32", (N + 63) / 64, (M + 63) / 64, 1, 256, &g, st, label);
+    if (p.K % 32) throw Error("mode F32 GEMM: K must be a multiple of 32");
+    c->launch("ltx_gemm_f32", (N + 127) / 128, (M + 127) / 128, 1, 256, &g, st, label);
 }
 
 static void qknorm32(ltx_ctx* c, float* x, const void* w, const float* cs, const float* sn, int rows, hipStream_t st) {

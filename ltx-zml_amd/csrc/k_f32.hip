@@ -1,66 +1,191 @@
-// f32 reference-precision kernels (mode LTX_MODE_F32): a SIMT tiled GEMM with
-// in-register dequant (f32(q) * s, exactly dq4 at ltx/block.zig:462-471) and an
-// online-softmax attention on f32 MFMAs. These carry the <= 1e-5 parity mode.
+// f32 reference-precision kernels (mode LTX_MODE_F32): a GEMM that dequantises
+// in f32 (f32(q) * s, exactly dq4 at ltx/block.zig:462-471) and an
+// online-softmax attention, both on f32 MFMAs. These carry the <= 1e-5 parity
+// mode.
 #include "ltx_device.h"
 
-// 64 x 64 output tile, 256 threads, 4 x 4 outputs per thread, K step 16.
-extern "C" __global__ void __launch_bounds__(256) ltx_gemm_f32(const LtxGemm32Args a) {
-    __shared__ float sA[16][64 + 1];
-    __shared__ float sB[16][64 + 1];
-    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-    const int G = a.K / LTX_GROUP;
-    float acc[4][4] = {};
-    for (int k0 = 0; k0 < a.K; k0 += 16) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            int id = tid + 256 * i, r = id >> 4, k = id & 15;
-            int m = min(m0 + r, a.M - 1);
-            sA[k][r] = a.a[(size_t)m * a.K + k0 + k];
-            int n = min(n0 + r, a.N - 1);
-            size_t bi = (size_t)n * a.K + k0 + k;
-            float bv;
-            if (a.bkind == 2) {
-                bv = bf16_bits_to_f32(((const uint16_t*)a.b)[bi]);
-            } else {
-                size_t si = (size_t)n * G + (k0 + k) / LTX_GROUP;
-                float s = a.bkind == 1 ? f16_bits_to_f32(((const uint16_t*)a.scales)[si]) : ((const float*)a.scales)[si];
-                bv = (float)((int)(((const uint8_t*)a.b)[bi] ^ (a.qxor & 0xffu)) - 128) * s;
-            }
-            sB[k][r] = bv;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            float av[4], bv[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) av[i] = sA[k][ty * 4 + i];
-#pragma unroll
-            for (int j = 0; j < 4; j++) bv[j] = sB[k][tx * 4 + j];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
-        }
-        __syncthreads();
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        int m = m0 + ty * 4 + i;
-        if (m >= a.M) continue;
+// y[M][N] = A[M][K] . W[N][K]^T (+ bias, GELU or the gated residual) in f32
+// on v_mfma_f32_16x16x4_f32. Workgroup: 4 waves, output tile 128 x 128, wave
+// w owns rows 64 (w / 2) .. +63 and columns 64 (w % 2) .. +63 (4 x 4 blocks
+// of 16 x 16). K goes in tiles of 32 through two LDS buffers: each tile's A
+// and W rows are loaded into registers while the previous tile is
+// multiplied, W dequantised as they are written to LDS (int8: f32(q) * s,
+// one f32 rounding, exactly dq4 at ltx/block.zig:462-471; bf16: widened).
+// In MFMA step s (0..7) the k index lg = lane / 16 stands for k = 8 lg + s,
+// so a lane's A and W operands of a tile are two float4 of one row. Rows are
+// padded to 36 floats: the 16 rows of a fragment read cover all 64 banks.
+// K must be a multiple of 32. BK is the weight kind (0: int8 + f32 scales,
+// 1: int8 + f16 scales, 2: bf16), RG the gated-residual epilogue; both are
+// compile-time so that no load in the main loop is conditional.
+__shared__ __attribute__((aligned(16))) float g32_sa[2][128 * 36];
+__shared__ __attribute__((aligned(16))) float g32_sb[2][128 * 36];
+
+template <int BK, bool RG>
+__device__ __forceinline__ void gemm32_body(const LtxGemm32Args& a) {
+    constexpr int LD = 36;
+    float(&sA)[2][128 * LD] = g32_sa;
+    float(&sB)[2][128 * LD] = g32_sb;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int m0 = blockIdx.y * 128, n0 = blockIdx.x * 128;
+    const int wm = (w >> 1) * 64, wn = (w & 1) * 64;
+    const int G = a.K / LTX_GROUP, ntile = a.K / 32;
+    // staging: A float4 f = tid + 256 j (row f / 8, chunk f % 8); W row
+    // tid / 2, k 16 (tid % 2) .. +15. Rows past M or N repeat the last one.
+    const int wr = tid >> 1, wk = 16 * (tid & 1);
+    const int wrow = min(n0 + wr, a.N - 1);
+    f32x4 pa[4];
+    u32x4 pw[BK == 2 ? 2 : 1];
+    uint32_t sraw = 0;  // the tile's scale, bits as stored
+    auto load = [&](int kt) {
+        const int k0 = 32 * kt;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            int n = n0 + tx * 4 + j;
-            if (n >= a.N) continue;
-            float v = acc[i][j] + (a.bias ? a.bias[n] : 0.0f);
-            size_t o = (size_t)m * a.N + n;
-            if (a.epi == LTX_EPI_RESID_GATE) {
-                a.out[o] = a.resid[o] + v * ada_val(a.ada, m, a.igate, n);
-            } else {
-                a.out[o] = a.gelu ? gelu_tanh(v) : v;
+            const int f = tid + 256 * j, r = f >> 3, c = f & 7;
+            pa[j] = *(const f32x4*)(a.a + (size_t)min(m0 + r, a.M - 1) * a.K + k0 + 4 * c);
+        }
+        const size_t bi = (size_t)wrow * a.K + k0 + wk;
+        if constexpr (BK == 2) {
+            pw[0] = *(const u32x4*)((const uint16_t*)a.b + bi);
+            pw[1] = *(const u32x4*)((const uint16_t*)a.b + bi + 8);
+        } else {
+            pw[0] = *(const u32x4*)((const uint8_t*)a.b + bi);
+            const size_t si = (size_t)wrow * G + k0 / LTX_GROUP;
+            if constexpr (BK == 1)
+                sraw = ((const uint16_t*)a.scales)[si];
+            else
+                sraw = ((const uint32_t*)a.scales)[si];
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int f = tid + 256 * j, r = f >> 3, c = f & 7;
+            *(f32x4*)(sA[buf] + r * LD + 4 * c) = pa[j];
+        }
+        float wv[16];
+        if constexpr (BK == 2) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t x = pw[i >> 2][i & 3];
+                wv[2 * i] = bf16_bits_to_f32((uint16_t)(x & 0xffffu));
+                wv[2 * i + 1] = bf16_bits_to_f32((uint16_t)(x >> 16));
+            }
+        } else {
+            const float sc = BK == 1 ? f16_bits_to_f32((uint16_t)sraw) : __builtin_bit_cast(float, sraw);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t byte = (pw[0][i >> 2] >> (8 * (i & 3))) & 0xffu;
+                wv[i] = (float)((int)(byte ^ (a.qxor & 0xffu)) - 128) * sc;
             }
         }
+        float* d = sB[buf] + wr * LD + wk;
+#pragma unroll
+        for (int i = 0; i < 4; i++) *(f32x4*)(d + 4 * i) = f32x4{wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]};
+    };
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+        for (int cb = 0; cb < 4; cb++) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kt = 0; kt < ntile; kt++) {
+        const int buf = kt & 1;
+        if (kt + 1 < ntile) load(kt + 1);
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            f32x4 af[4], bf[4];
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++) af[rb] = *(const f32x4*)(sA[buf] + (wm + 16 * rb + lr) * LD + 8 * lg + 4 * hh);
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++) bf[cb] = *(const f32x4*)(sB[buf] + (wn + 16 * cb + lr) * LD + 8 * lg + 4 * hh);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                    for (int cb = 0; cb < 4; cb++)
+                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[rb][e], bf[cb][e], acc[rb][cb], 0, 0, 0);
+        }
+        // the other buffer was last read in the previous trip, before its
+        // closing barrier
+        if (kt + 1 < ntile) store(buf ^ 1);
+        __syncthreads();
     }
+    // acc[rb][cb][r]: row wm + 16 rb + 4 lg + r, column wn + 16 cb + lr.
+    // The residual and gate values of a row block are loaded before its
+    // first store (rows and columns past M and N load the last ones).
+    int nc[4];
+    float bv[4], sv[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; cb++) {
+        nc[cb] = min(n0 + wn + 16 * cb + lr, a.N - 1);
+        bv[cb] = a.bias ? a.bias[nc[cb]] : 0.0f;
+        if constexpr (RG) sv[cb] = a.ada.sst[(size_t)a.igate * LTX_D + nc[cb]];
+    }
+    const bool full = m0 + 128 <= a.M && n0 + 128 <= a.N;
+    int trow[4][4];  // timestep-table row of each output row
+    if constexpr (RG) {
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) trow[rb][r] = ada_row(a.ada, min(m0 + wm + 16 * rb + 4 * lg + r, a.M - 1));
+    }
+#pragma unroll
+    for (int rb = 0; rb < 4; rb++) {
+        float rv[4][4], gv[4][4];
+        if constexpr (RG) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int mc = min(m0 + wm + 16 * rb + 4 * lg + r, a.M - 1);
+                const float* tr = a.ada.tstab + ((size_t)trow[rb][r] * 9 + a.igate) * LTX_D;
+#pragma unroll
+                for (int cb = 0; cb < 4; cb++) {
+                    rv[r][cb] = a.resid[(size_t)mc * a.N + nc[cb]];
+                    gv[r][cb] = tr[nc[cb]] + sv[cb];  // the AdaLN gate value, as ada_val
+                }
+            }
+        }
+        float val[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++) {
+                const float v = acc[rb][cb][r] + bv[cb];
+                if constexpr (RG)
+                    val[r][cb] = rv[r][cb] + v * gv[r][cb];
+                else
+                    val[r][cb] = a.gelu ? gelu_tanh(v) : v;
+            }
+        // whole tiles store without per-element branches (each branch join
+        // would otherwise wait for the stores before it)
+        float* orow = a.out + (size_t)(m0 + wm + 16 * rb + 4 * lg) * a.N + n0 + wn + lr;
+        if (full) {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int cb = 0; cb < 4; cb++) orow[(size_t)r * a.N + 16 * cb] = val[r][cb];
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int cb = 0; cb < 4; cb++)
+                    if (m0 + wm + 16 * rb + 4 * lg + r < a.M && n0 + wn + 16 * cb + lr < a.N)
+                        orow[(size_t)r * a.N + 16 * cb] = val[r][cb];
+        }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) ltx_gemm_f32(const LtxGemm32Args a) {
+    const bool rg = a.epi == LTX_EPI_RESID_GATE;
+    if (a.bkind == 0)
+        rg ? gemm32_body<0, true>(a) : gemm32_body<0, false>(a);
+    else if (a.bkind == 1)
+        rg ? gemm32_body<1, true>(a) : gemm32_body<1, false>(a);
+    else
+        rg ? gemm32_body<2, true>(a) : gemm32_body<2, false>(a);
 }
 
 // f32 flash attention on v_mfma_f32_16x16x4_f32 (the f32 arithmetic of
