@@ -449,8 +449,8 @@ def main() -> int:
     mode = rt.MODES[args.mode]
     stream = torch.cuda.current_stream()
 
-    def step():
-        ctx.forward(w, x, tstab, tidx, c, pts2, dcos, dsin, y, mode=mode, stream=stream)
+    def step(out=y):
+        ctx.forward(w, x, tstab, tidx, c, pts2, dcos, dsin, out, mode=mode, stream=stream)
 
     if args.copy_calib_mib:
         src = torch.empty(args.copy_calib_mib << 18, dtype=torch.float32, device="cuda").fill_(1.0)
@@ -461,19 +461,34 @@ def main() -> int:
         del src, dst
     for _ in range(args.warmup):
         step()
+    # the timed forward is the ltx_block_forward call; the same forward
+    # captured once into a HIP graph (ltx_block_graph_create) and replayed
+    # per step is timed beside it
+    graph = ctx.block_graph(w, x, tstab, tidx, c, pts2, dcos, dsin, y, mode=mode)
+    graph.launch(stream)
     log("bench: warmup done")
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
-    # the output check after the timed region: between the warm-up and the
+
+    def timed(fn, n):
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    ms = timed(step, args.steps)
+    ms_graph = timed(lambda: graph.launch(stream), args.steps)
+    # the output checks after the timed region: between the warm-up and the
     # timed forwards its 470 MB read and 117 MB mask slowed the first timed
     # forwards (22.18 against 21.87 ms per forward over the first ten)
     assert torch.isfinite(y).all().item(), "non-finite block output"
+    y_graph = y.clone()
+    step()
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), y_graph.view(torch.int32)), "graph replay differs from the eager forward"
+    del y_graph
     # per-kernel times of the same forward in a separate pass (the events
     # around each launch stay out of the timed region): per forward, summed
     # over a label's launches
@@ -490,7 +505,7 @@ def main() -> int:
     attn_ms = per["attn:self"]
     achieved = f["self_attn"] / (attn_ms * 1e-3) / 1e12
     gemm_ms = sum(v for k, v in per.items() if k.startswith("gemm:"))
-    log(f"bench: block {ms:.2f} ms, self-attn {attn_ms:.2f} ms, GEMMs {gemm_ms:.2f} ms")
+    log(f"bench: block {ms:.2f} ms (as a graph {ms_graph:.2f} ms), self-attn {attn_ms:.2f} ms, GEMMs {gemm_ms:.2f} ms")
     res = {
         "metric": "int8 DiT-block ms + % bf16 MFMA peak @28,672 tok; attention TFLOP/s",
         "value": round(total / (ms * 1e-3) / 1e12, 2),
@@ -506,6 +521,8 @@ def main() -> int:
                    "text_tokens": S, "d_model": D, "heads": H, "head_dim": HD, "ffn": FF, "sigma": 0.7,
                    "batch": 1, "step": "one block forward"},
         "block_ms": round(ms, 3),
+        "graph_block_ms": round(ms_graph, 3),
+        "launch": "ltx_block_forward per step; graph_block_ms: the same forward as a HIP graph (ltx_block_graph_launch)",
         "pct_bf16_dense_peak": round(100.0 * total / (ms * 1e-3) / 1e12 / PEAK_TFLOPS, 2),
         "attention_tflops": round(achieved, 1),
         "gemm_tflops": round(f["gemm"] / (gemm_ms * 1e-3) / 1e12, 1) if gemm_ms else None,
@@ -523,6 +540,7 @@ def main() -> int:
                                + " (self-attention, 4*H*T^2*HD = "
                                f"{f['self_attn'] / 1e12:.3f} TFLOP per launch)"},
     }
+    graph.free()
     w.free()
     # the reference's CPU-runnable configuration: T = 1,024 on (4, 16, 16),
     # S = 128, N(0, 0.02) weights with fp16 scales, sigma 0.5 (after the
@@ -541,13 +559,11 @@ def main() -> int:
 
     for _ in range(3):
         step0()
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(20):
-        step0()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    res["t1024_block_ms"] = round(e0.elapsed_time(e1) / 20, 4)
+    graph0 = ctx.block_graph(w0, d0["x"], d0["tstab"], d0["tidx"], d0["ctx"], d0["pts2"], dc0, ds0, y0, mode=mode)
+    graph0.launch(stream)
+    res["t1024_block_ms"] = round(timed(step0, 20), 4)
+    res["t1024_graph_block_ms"] = round(timed(lambda: graph0.launch(stream), 20), 4)
+    graph0.free()
     ctx.profile(True)  # per-kernel times of the same forward, in a separate pass
     ctx.profile_reset()
     for _ in range(5):

@@ -125,6 +125,28 @@ int ltx_block_forward(ltx_ctx* ctx, const ltx_block_weights* w, const float* x, 
                       const int32_t* tidx, const float* ctx_tokens, int S, const float* pts2, const float* cos,
                       const float* sin, int T, float* y, int mode, void* stream);
 
+/* The same forward captured once and replayed: the pair the reference's
+ * caller uses, platform.compile binding the method into an executable
+ * (ltx/e2e_prod.zig:297-299) and exe.call per block (ltx/e2e_prod.zig:377-399),
+ * here as a HIP graph with the buffers bound at creation.
+ * ltx_block_graph_create runs no kernel: it sizes the context's workspace and
+ * records one ltx_block_forward with these arguments (same meanings) into a
+ * graph. ltx_block_graph_launch enqueues that forward on `stream`,
+ * asynchronously, with the same results bit for bit; it saves the launch
+ * overhead between the forward's kernels.
+ * The graph binds the weights, every buffer and the context's workspace:
+ * they must outlive it, and while a graph lives, a forward on the context
+ * that needs a larger workspace fails. Launches share the workspace with
+ * every other forward on the context: in order on one stream, racing on
+ * different streams. Event profiling must be off at creation, and graph
+ * launches are not profiled. Destroy graphs before their context. */
+typedef struct ltx_block_graph ltx_block_graph;
+int ltx_block_graph_create(ltx_ctx* ctx, const ltx_block_weights* w, const float* x, const float* tstab, int K,
+                           const int32_t* tidx, const float* ctx_tokens, int S, const float* pts2, const float* cos,
+                           const float* sin, int T, float* y, int mode, ltx_block_graph** out);
+int ltx_block_graph_launch(ltx_block_graph* g, void* stream);
+void ltx_block_graph_destroy(ltx_block_graph* g);
+
 /* Intermediate tensors of the last forward, for staged parity checks
  * (the staged methods of ltx/block.zig:248-338), and the velocity of the last
  * ltx_denoise step (ltx/e2e_denoise.zig:314 gates it per step). Device

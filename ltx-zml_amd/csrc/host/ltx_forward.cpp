@@ -110,6 +110,9 @@ static void ensure_ws(ltx_ctx* c, size_t T, size_t S, int mode) {
         carve16(cv, w, T, S, c->num_cu);
     }
     if (c->ws.bytes < cv.off) {
+        if (c->ws_pins)
+            throw Error("the workspace is bound by " + std::to_string(c->ws_pins) +
+                        " live block graph(s) and this forward needs a larger one; destroy them first");
         HIPC(hipDeviceSynchronize());
         c->ws.alloc(cv.off);
     }
@@ -575,6 +578,77 @@ int ltx_block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, co
         if (!c) throw ltx::Error("NULL context");
         ltx::block_forward(c, w, x, tstab, K, tidx, ctx_tokens, S, pts2, cos, sin, T, y, mode, (hipStream_t)stream);
     })
+}
+
+// A block forward captured once into a HIP graph, with its buffers bound.
+struct ltx_block_graph {
+    ltx_ctx* c = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+int ltx_block_graph_create(ltx_ctx* c, const ltx_block_weights* w, const float* x, const float* tstab, int K,
+                           const int32_t* tidx, const float* ctx_tokens, int S, const float* pts2, const float* cos,
+                           const float* sin, int T, float* y, int mode, ltx_block_graph** out) {
+    LTX_GUARD(c, {
+        if (!c) throw ltx::Error("NULL context");
+        if (!out) throw ltx::Error("NULL output handle");
+        *out = nullptr;
+        if (c->prof) throw ltx::Error("event profiling is on; a graph cannot capture its events");
+        if (T <= 0 || S <= 0) throw ltx::Error("bad token counts");
+        HIPC(hipSetDevice(c->device));
+        // the workspace is sized (and allocated) before the capture, which
+        // may only record launches and event waits
+        ltx::ensure_ws(c, (size_t)T, (size_t)S, mode);
+        hipStream_t cs = nullptr;
+        HIPC(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking));
+        hipGraph_t graph = nullptr;
+        HIPC(hipStreamBeginCapture(cs, hipStreamCaptureModeRelaxed));
+        try {
+            ltx::block_forward(c, w, x, tstab, K, tidx, ctx_tokens, S, pts2, cos, sin, T, y, mode, cs);
+        } catch (...) {
+            (void)hipStreamEndCapture(cs, &graph);
+            if (graph) (void)hipGraphDestroy(graph);
+            (void)hipStreamDestroy(cs);
+            throw;
+        }
+        const hipError_t ec = hipStreamEndCapture(cs, &graph);
+        (void)hipStreamDestroy(cs);
+        if (ec != hipSuccess || !graph) {
+            if (graph) (void)hipGraphDestroy(graph);
+            throw ltx::Error(std::string("graph capture of the block forward failed: ") + hipGetErrorString(ec));
+        }
+        hipGraphExec_t exec = nullptr;
+        const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (ei != hipSuccess) {
+            (void)hipGraphDestroy(graph);
+            throw ltx::Error(std::string("graph instantiation failed: ") + hipGetErrorString(ei));
+        }
+        ltx_block_graph* g = new ltx_block_graph;
+        g->c = c;
+        g->graph = graph;
+        g->exec = exec;
+        c->ws_pins++;
+        *out = g;
+    })
+}
+
+int ltx_block_graph_launch(ltx_block_graph* g, void* stream) {
+    ltx_ctx* c = g ? g->c : nullptr;
+    LTX_GUARD(c, {
+        if (!g) throw ltx::Error("NULL graph");
+        HIPC(hipSetDevice(c->device));
+        HIPC(hipGraphLaunch(g->exec, (hipStream_t)stream));
+    })
+}
+
+void ltx_block_graph_destroy(ltx_block_graph* g) {
+    if (!g) return;
+    (void)hipSetDevice(g->c->device);
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    g->c->ws_pins--;
+    delete g;
 }
 
 int ltx_op_linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* scales, int scale_f16, const float* bias,

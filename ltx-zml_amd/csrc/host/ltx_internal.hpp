@@ -106,6 +106,7 @@ struct ltx_ctx {
     ltx::DevBuf dn_ws;     // the denoising loop's activations
     size_t ws_T = 0, ws_S = 0;
     int ws_mode = -1;
+    int ws_pins = 0;  // live block graphs: their kernels hold workspace addresses
     void* stage_ptr[LTX_ST_COUNT] = {};
     uint64_t stage_bytes[LTX_ST_COUNT] = {};
     // profiling

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes as C
 import pathlib
+import weakref
 
 import numpy as np
 
@@ -51,6 +52,9 @@ def lib() -> C.CDLL:
         "ltx_block_weights_free": (None, [vp, vp]),
         "ltx_block_weights_bytes": (u64, [vp]),
         "ltx_block_forward": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, vp, vp, vp, i32, vp, i32, vp]),
+        "ltx_block_graph_create": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, vp, vp, vp, i32, vp, i32, C.POINTER(vp)]),
+        "ltx_block_graph_launch": (i32, [vp, vp]),
+        "ltx_block_graph_destroy": (None, [vp]),
         "ltx_block_stage": (i32, [vp, i32, C.POINTER(vp), C.POINTER(u64)]),
         "ltx_range_count": (i32, [vp, vp, C.POINTER(u64), i32]),
         "ltx_op_linear_q8": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
@@ -173,6 +177,31 @@ class Weights:
             pass
 
 
+class BlockGraph:
+    """One block forward captured with its buffers bound (ltx_block_graph_*);
+    launch() replays it on a stream."""
+
+    def __init__(self, ctx: "Context", handle: int, keep: tuple):
+        self.ctx, self.handle = ctx, handle
+        self._keep = keep  # the bound tensors stay alive with the graph
+
+    def launch(self, stream=None):
+        st = stream.cuda_stream if stream is not None else _current_stream()
+        self.ctx._check(lib().ltx_block_graph_launch(self.handle, st), "ltx_block_graph_launch")
+
+    def free(self):
+        if self.handle:
+            lib().ltx_block_graph_destroy(self.handle)
+            self.handle = None
+            self._keep = ()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class Context:
     """One device context (ltx_init). Not thread-safe."""
 
@@ -182,6 +211,7 @@ class Context:
             raise LtxError("ltx_init: " + lib().ltx_last_error(None).decode())
         self.handle = h.value
         self.device = device
+        self._graphs = weakref.WeakSet()
 
     def _check(self, ok: int, what: str):
         if not ok:
@@ -189,6 +219,8 @@ class Context:
 
     def close(self):
         if self.handle:
+            for g in list(self._graphs):  # graphs hold the context's workspace
+                g.free()
             lib().ltx_destroy(self.handle)
             self.handle = None
 
@@ -236,6 +268,18 @@ class Context:
                                             _ptr(pts2), _ptr(cos), _ptr(sin), T, _ptr(y), mode, st),
                     "ltx_block_forward")
         return y
+
+    def block_graph(self, w: Weights, x, tstab, tidx, ctx, pts2, cos, sin, y, mode: int = MODE_F16) -> BlockGraph:
+        """The forward of ``forward`` with these tensors, captured once
+        (ltx_block_graph_create); BlockGraph.launch() runs it."""
+        T, S, K = x.shape[0], ctx.shape[0], tstab.shape[0]
+        h = C.c_void_p()
+        self._check(lib().ltx_block_graph_create(self.handle, w.handle, _ptr(x), _ptr(tstab), K, _ptr(tidx), _ptr(ctx),
+                                                 S, _ptr(pts2), _ptr(cos), _ptr(sin), T, _ptr(y), mode, C.byref(h)),
+                    "ltx_block_graph_create")
+        g = BlockGraph(self, h.value, (w, x, tstab, tidx, ctx, pts2, cos, sin, y))
+        self._graphs.add(g)
+        return g
 
     def range_count(self, reset: bool = True, stream=None) -> int:
         """16-bit stores out of range since the last reset (ltx_range_count)."""

@@ -1,0 +1,100 @@
+"""The block forward captured as a HIP graph (ltx_block_graph_*): every replay
+equals the eager ltx_block_forward bit for bit, with eager forwards and
+synchronisations between the replays; a live graph pins the context's
+workspace; capture is refused while event profiling is on."""
+import numpy as np
+import pytest
+
+from conftest import say
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+from ltx_amd import runtime as rt  # noqa: E402
+from ltx_amd import synth  # noqa: E402
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _inputs(T, S):
+    inp = synth.make_inputs(T, S, sigma=0.7)
+    cos, sin = rt.rope_tables(inp["grid"])
+    d = {k: dev(inp[k]) for k in ("x", "tstab", "tidx", "ctx", "pts2")}
+    return d, dev(cos), dev(sin)
+
+
+def _eager(ctx, w, d, cos, sin, y, mode):
+    ctx.forward(w, d["x"], d["tstab"], d["tidx"], d["ctx"], d["pts2"], cos, sin, y, mode=mode)
+
+
+@pytest.mark.parametrize("mode,T,S", [("f16", 256, 64), ("f16", 250, 40), ("bf16", 256, 64), ("f32", 128, 32)])
+def test_block_graph_matches_eager(ctx, block0, mode, T, S):
+    say(f"block graph mode={mode} T={T} S={S}")
+    md = rt.MODES[mode]
+    w = ctx.upload(block0)
+    d, cos, sin = _inputs(T, S)
+    y_ref = torch.empty((T, 4096), dtype=torch.float32, device="cuda")
+    _eager(ctx, w, d, cos, sin, y_ref, md)
+    torch.cuda.synchronize()
+    want = y_ref.clone()
+    y = torch.full((T, 4096), float("nan"), dtype=torch.float32, device="cuda")
+    g = ctx.block_graph(w, d["x"], d["tstab"], d["tidx"], d["ctx"], d["pts2"], cos, sin, y, mode=md)
+    try:
+        torch.cuda.synchronize()
+        assert torch.isnan(y).all(), "creating the graph ran kernels"
+        for i in range(3):
+            y.fill_(float("nan"))
+            g.launch()
+            torch.cuda.synchronize()
+            assert torch.equal(y.view(torch.int32), want.view(torch.int32)), f"replay {i}"
+            # the context's own eager work between the replays
+            _eager(ctx, w, d, cos, sin, y_ref, md)
+            torch.cuda.synchronize()
+            assert torch.equal(y_ref.view(torch.int32), want.view(torch.int32)), f"eager after replay {i}"
+        # replays back to back on one stream
+        for _ in range(3):
+            g.launch()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), want.view(torch.int32))
+    finally:
+        g.free()  # a live graph pins the shared context's workspace
+        w.free()
+
+
+def test_block_graph_pins_workspace(block0):
+    say("block graph workspace pin")
+    c = rt.Context(0)
+    try:
+        w = c.upload(block0)
+        d, cos, sin = _inputs(64, 16)
+        y = torch.empty((64, 4096), dtype=torch.float32, device="cuda")
+        g = c.block_graph(w, d["x"], d["tstab"], d["tidx"], d["ctx"], d["pts2"], cos, sin, y, mode=rt.MODE_F16)
+        g.launch()
+        torch.cuda.synchronize()
+        d2, cos2, sin2 = _inputs(512, 16)
+        y2 = torch.empty((512, 4096), dtype=torch.float32, device="cuda")
+        with pytest.raises(rt.LtxError, match="workspace"):
+            _eager(c, w, d2, cos2, sin2, y2, rt.MODE_F16)
+        g.free()
+        _eager(c, w, d2, cos2, sin2, y2, rt.MODE_F16)
+        torch.cuda.synchronize()
+        assert torch.isfinite(y2).all()
+        w.free()
+    finally:
+        c.close()
+
+
+def test_block_graph_refused_while_profiling(ctx, block0):
+    say("block graph refused while profiling")
+    w = ctx.upload(block0)
+    d, cos, sin = _inputs(64, 16)
+    y = torch.empty((64, 4096), dtype=torch.float32, device="cuda")
+    ctx.profile(True)
+    try:
+        with pytest.raises(rt.LtxError, match="profiling"):
+            ctx.block_graph(w, d["x"], d["tstab"], d["tidx"], d["ctx"], d["pts2"], cos, sin, y, mode=rt.MODE_F16)
+    finally:
+        ctx.profile(False)
+    w.free()
