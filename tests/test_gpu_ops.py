@@ -180,15 +180,22 @@ def test_linear_q8_variants(monkeypatch, variant):
         c.close()
 
 
-def test_linear_q8_f32_mode(ctx):
-    say("linear_q8 mode=f32 M=200 N=384 K=2048")
-    a, q, s, b = _gemm_case(200, 384, 2048, seed=5)
-    y = torch.empty((200, 384), dtype=torch.float32, device="cuda")
+# the f32 MFMA GEMM: f32 and f16 scales, ragged M and N (partial 128 x 128
+# tiles), GELU, one row and one K group
+@pytest.mark.parametrize("M,N,K,scale_f16,gelu", [(200, 384, 2048, False, False), (200, 384, 2048, True, False),
+                                                  (333, 200, 4096, True, True), (1, 130, 128, False, False)])
+def test_linear_q8_f32_mode(ctx, M, N, K, scale_f16, gelu):
+    say(f"linear_q8 mode=f32 M={M} N={N} K={K} scale_f16={scale_f16} gelu={gelu}")
+    a, q, s, b = _gemm_case(M, N, K, seed=5 + M + N, scale_f16=scale_f16)
+    y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
     ctx.linear_q8(torch.from_numpy(a).cuda(), torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(),
-                  torch.from_numpy(b).cuda(), y, mode=rt.MODE_F32)
+                  torch.from_numpy(b).cuda(), y, mode=rt.MODE_F32, gelu=gelu)
     torch.cuda.synchronize()
-    want = oracle.linear(a, q=q, s=s) + b
-    assert oracle.rel_rms(f64(y), want) <= 1e-6
+    z = oracle.linear(a, q=q, s=s.astype(np.float32)) + b
+    want = 0.5 * z * (1 + np.tanh(np.sqrt(2 / np.pi) * (z + 0.044715 * z ** 3))) if gelu else z
+    # the products alone to 1e-6; the device GELU (tanh through the fast exp
+    # and reciprocal) to the f32 mode's 1e-5
+    assert oracle.rel_rms(f64(y), want) <= (1e-5 if gelu else 1e-6)
 
 
 def _heads(x, L):  # [L, D] -> [H, L, 128]
