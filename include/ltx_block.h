@@ -131,15 +131,18 @@ int ltx_block_forward(ltx_ctx* ctx, const ltx_block_weights* w, const float* x, 
  * here as a HIP graph with the buffers bound at creation.
  * ltx_block_graph_create runs no kernel: it sizes the context's workspace and
  * records one ltx_block_forward with these arguments (same meanings) into a
- * graph. ltx_block_graph_launch enqueues that forward on `stream`,
- * asynchronously, with the same results bit for bit; it saves the launch
- * overhead between the forward's kernels.
+ * graph. ltx_block_graph_launch enqueues that forward on `stream` with one
+ * host call, asynchronously, with the same results bit for bit (measured:
+ * no faster than ltx_block_forward at 28,672 tokens; for callers that
+ * replay or capture).
  * The graph binds the weights, every buffer and the context's workspace:
  * they must outlive it, and while a graph lives, a forward on the context
  * that needs a larger workspace fails. Launches share the workspace with
  * every other forward on the context: in order on one stream, racing on
  * different streams. Event profiling must be off at creation, and graph
- * launches are not profiled. Destroy graphs before their context. */
+ * launches are not profiled. After a launch, ltx_block_stage reads the
+ * intermediates of the captured forward. Destroy graphs before their
+ * context. */
 typedef struct ltx_block_graph ltx_block_graph;
 int ltx_block_graph_create(ltx_ctx* ctx, const ltx_block_weights* w, const float* x, const float* tstab, int K,
                            const int32_t* tidx, const float* ctx_tokens, int S, const float* pts2, const float* cos,

@@ -585,6 +585,10 @@ struct ltx_block_graph {
     ltx_ctx* c = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    // the captured forward's intermediates, restored for ltx_block_stage at
+    // every launch
+    void* stage_ptr[LTX_ST_COUNT] = {};
+    uint64_t stage_bytes[LTX_ST_COUNT] = {};
 };
 
 int ltx_block_graph_create(ltx_ctx* c, const ltx_block_weights* w, const float* x, const float* tstab, int K,
@@ -628,6 +632,8 @@ int ltx_block_graph_create(ltx_ctx* c, const ltx_block_weights* w, const float* 
         g->c = c;
         g->graph = graph;
         g->exec = exec;
+        std::memcpy(g->stage_ptr, c->stage_ptr, sizeof(g->stage_ptr));
+        std::memcpy(g->stage_bytes, c->stage_bytes, sizeof(g->stage_bytes));
         c->ws_pins++;
         *out = g;
     })
@@ -639,6 +645,8 @@ int ltx_block_graph_launch(ltx_block_graph* g, void* stream) {
         if (!g) throw ltx::Error("NULL graph");
         HIPC(hipSetDevice(c->device));
         HIPC(hipGraphLaunch(g->exec, (hipStream_t)stream));
+        std::memcpy(c->stage_ptr, g->stage_ptr, sizeof(c->stage_ptr));
+        std::memcpy(c->stage_bytes, g->stage_bytes, sizeof(c->stage_bytes));
     })
 }
 

@@ -58,6 +58,14 @@ def test_block_graph_matches_eager(ctx, block0, mode, T, S):
             g.launch()
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int32), want.view(torch.int32))
+        # after an eager forward of another size, a launch restores the
+        # captured forward's intermediates for ltx_block_stage
+        d2, cos2, sin2 = _inputs(64, 16)
+        y2 = torch.empty((64, 4096), dtype=torch.float32, device="cuda")
+        _eager(ctx, w, d2, cos2, sin2, y2, md)
+        g.launch()
+        torch.cuda.synchronize()
+        assert ctx.stage("x_sa").numel() == T * 4096 * 4
     finally:
         g.free()  # a live graph pins the shared context's workspace
         w.free()
