@@ -4,6 +4,7 @@
 #include <cmath>
 #include <algorithm>
 #include <cstring>
+#include <new>
 
 #include "ltx_internal.hpp"
 
@@ -607,7 +608,11 @@ int ltx_block_graph_create(ltx_ctx* c, const ltx_block_weights* w, const float* 
         hipStream_t cs = nullptr;
         HIPC(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking));
         hipGraph_t graph = nullptr;
-        HIPC(hipStreamBeginCapture(cs, hipStreamCaptureModeRelaxed));
+        const hipError_t eb = hipStreamBeginCapture(cs, hipStreamCaptureModeRelaxed);
+        if (eb != hipSuccess) {
+            (void)hipStreamDestroy(cs);
+            throw ltx::Error(std::string("graph capture could not start: ") + hipGetErrorString(eb));
+        }
         try {
             ltx::block_forward(c, w, x, tstab, K, tidx, ctx_tokens, S, pts2, cos, sin, T, y, mode, cs);
         } catch (...) {
@@ -628,7 +633,12 @@ int ltx_block_graph_create(ltx_ctx* c, const ltx_block_weights* w, const float* 
             (void)hipGraphDestroy(graph);
             throw ltx::Error(std::string("graph instantiation failed: ") + hipGetErrorString(ei));
         }
-        ltx_block_graph* g = new ltx_block_graph;
+        ltx_block_graph* g = new (std::nothrow) ltx_block_graph;
+        if (!g) {
+            (void)hipGraphExecDestroy(exec);
+            (void)hipGraphDestroy(graph);
+            throw ltx::Error("out of host memory");
+        }
         g->c = c;
         g->graph = graph;
         g->exec = exec;
