@@ -153,14 +153,17 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
     return s;
 }
 
-// GELU, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))),
-// with tanh(u) = 1 - 2 / (exp(2u) + 1) (exact identity; saturates cleanly).
+// GELU, tanh form: 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3),
+// evaluated through the exact identity 0.5 (1 + tanh u) = 1 / (1 + exp(-2u)):
+// x / (1 + 2^(-2u log2 e)). No subtraction, so no cancellation for negative
+// x (the form 1 - 2 / (exp(2u) + 1) lost most digits of 1 + tanh u there),
+// and 8 VALU operations against 12 (the ff1 GEMM 1.2 % faster). Large
+// negative x gives -0 (exp overflows to inf), large positive x gives x.
 __device__ __forceinline__ float gelu_tanh(float x) {
     const float c = 0.7978845608028654f;
-    float u = c * (x + 0.044715f * x * x * x);
-    float e = __expf(2.0f * u);
-    float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-    return 0.5f * x * (1.0f + t);
+    const float a = x * __builtin_fmaf(0.044715f * x, x, 1.0f);  // x + 0.044715 x^3
+    const float e = __builtin_amdgcn_exp2f(a * (-2.0f * c * 1.4426950408889634f));
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + __expf(-x)); }
