@@ -414,8 +414,9 @@ def main() -> int:
                          "(the known-size kernel that calibrates HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "single-GPU build: the block runs on one MI355X; multi-GPU sharding is a "
-                                   "design (DESIGN.md), not part of this benchmark", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "single-GPU build: the block runs on one MI355X; how it would shard across "
+                                   "GPUs is designed but not built, and not part of this benchmark",
+                          "n_gpus": args.gpus}))
         return 2
 
     import numpy as np

@@ -170,7 +170,7 @@ int main(int argc, char** argv) {
             if (hipEventSynchronize(e1) != hipSuccess) return 2;
             float t = 0.0f;
             hipEventElapsedTime(&t, e0, e1);
-            if (rep) ms[i].push_back(t);  // round 0 warms up
+            if (rep) ms[i].push_back(t);  // the first repetition warms up
         }
     for (int i = 0; i < NV; i++) {
         std::sort(ms[i].begin(), ms[i].end());
