@@ -289,6 +289,34 @@ def test_attention_special_cases(ctx, lkv, dom, q_scaled):
     assert np.abs(f64(out) - vd[None, :]).max() < 5e-3
 
 
+@pytest.mark.parametrize("lkv,dom", [(96, 70), (200, 130), (256, 200), (1000, 900)])
+def test_attention_f32_special_cases(ctx, lkv, dom):
+    """The f32 MFMA attention: identical keys -> the mean of V; one dominant
+    key past the first 64-key tiles -> that V row (the running max moves and
+    O is rescaled); key counts that are not multiples of 64 mask the last
+    tile."""
+    say(f"attention special cases f32 lkv={lkv} dominant key={dom}")
+    rng = np.random.default_rng(13 + lkv)
+    lq = 70
+    q = rng.standard_normal((lq, 4096)).astype(np.float32)
+    k = np.tile(rng.standard_normal((1, 4096)).astype(np.float32), (lkv, 1))
+    v = rng.standard_normal((lkv, 4096)).astype(np.float32)
+    out = torch.empty((lq, 4096), dtype=torch.float32, device="cuda")
+    dv = torch.from_numpy(v).cuda()
+    ctx.attention(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), dv, None, out, lq, lkv, mode=rt.MODE_F32)
+    torch.cuda.synchronize()
+    vm = v.astype(np.float64).mean(0)
+    assert np.abs(f64(out) - vm[None, :]).max() < 1e-5
+    # key `dom` is 4 q in every head: its score leads the others by ~45 in
+    # natural-log units, so the softmax is one-hot to f32 precision
+    k2 = rng.standard_normal((lkv, 4096)).astype(np.float32) * 0.01
+    qq = np.tile(rng.standard_normal((1, 4096)).astype(np.float32), (lq, 1))
+    k2[dom] = qq[0] * 4.0
+    ctx.attention(torch.from_numpy(qq).cuda(), torch.from_numpy(k2).cuda(), dv, None, out, lq, lkv, mode=rt.MODE_F32)
+    torch.cuda.synchronize()
+    assert np.abs(f64(out) - v[dom].astype(np.float64)[None, :]).max() < 1e-5
+
+
 @pytest.mark.parametrize("variant,lq,lkv", [("w8", 384, 2048), ("default", 384, 2048), ("pp", 1000, 256),
                                             ("default", 1000, 256)])
 def test_attention_variants(monkeypatch, variant, lq, lkv):
