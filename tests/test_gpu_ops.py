@@ -141,6 +141,28 @@ def test_linear_q8_onehot_exact(ctx, M, N, K, mode, sf32):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("sf32,exp_range", [(True, (-4, -1)), (False, (-4, -1)), (True, (-30, 30))])
+def test_linear_q8_onehot_exact_f32_mode(ctx, sf32, exp_range):
+    """The f32 MFMA GEMM on one-hot rows: every output is one dequantised
+    weight times 1 (one nonzero product, f32 accumulation), so y must equal
+    f32(q) * s (dq4 at ltx/block.zig:462-471) bit for bit, f32 or f16 scales,
+    and scales across 60 decades."""
+    say(f"linear_q8 one-hot f32 mode f32 scales={sf32} 1e{exp_range[0]}..1e{exp_range[1]}")
+    M, N, K = 300, 256, 512
+    rng = np.random.default_rng(31 + K)
+    q = rng.integers(-128, 128, size=(N, K), dtype=np.int16).astype(np.int8)
+    s = (10.0 ** rng.uniform(*exp_range, size=(N, K // 128))).astype(np.float32 if sf32 else np.float16)
+    e = np.zeros((M, K), np.float32)
+    e[np.arange(M), np.arange(M) % K] = 1.0
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    ctx.linear_q8(torch.from_numpy(e).cuda(), torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(), None, y,
+                  mode=rt.MODE_F32)
+    torch.cuda.synchronize()
+    want = oracle.dequant(q, s)[:, np.arange(M) % K].T
+    got = y.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), np.ascontiguousarray(want).view(np.uint32))
+
+
 @pytest.mark.parametrize("mode,exp_range", [
     ("f16", (-9, -5)),   # q * s among the f16 subnormals: one rounding into them
     ("bf16", (20, 36)),  # q * s up to 1.3e38: the bf16 path keeps the whole f32 range
