@@ -59,6 +59,8 @@ def lib(real: str = "f64") -> C.CDLL:
     L.orc_sdpa.restype = i32
     L.orc_linear.argtypes = [vp, i32, i32, vp, vp, vp, i32, vp, i32, vp]
     L.orc_rms.argtypes = [vp, i32, i32, vp, vp]
+    L.orc_rope_apply.argtypes = [vp, i32, vp, vp]
+    L.orc_gelu.argtypes = [vp, C.c_long, vp]
     _libs[real] = L
     return L
 
@@ -124,6 +126,37 @@ def linear(x, w_bf16=None, q=None, s=None, b_bf16=None, real: str = "f64"):
     y = np.empty((M, N), dt)
     sf16 = int(s is not None and s.dtype == np.float16)
     lib(real).orc_linear(x.ctypes.data, M, K, _p(w_bf16), _p(q), _p(s), sf16, _p(b_bf16), N, y.ctypes.data)
+    return y
+
+
+def rms(x, w_bf16=None, real: str = "f64"):
+    """rmsNoW / rmsW rows (ltx/block.zig:28-34); w_bf16 the norm weight as bf16 bits."""
+    dt = _rdt(real)
+    x = np.ascontiguousarray(x, dt)
+    y = np.empty_like(x)
+    w = None if w_bf16 is None else np.ascontiguousarray(w_bf16, np.uint16)
+    lib(real).orc_rms(x.ctypes.data, x.shape[0], x.shape[1], _p(w), y.ctypes.data)
+    return y
+
+
+def rope_apply(x, cos_thf, sin_thf, real: str = "f64"):
+    """Split-half RoPE (ltx/block.zig:69-77) of x [T, 4096] with graph-layout
+    cos/sin [T, 32, 64] f32; returns a new array."""
+    dt = _rdt(real)
+    y = np.array(x, dt, order="C", copy=True)
+    cs = np.ascontiguousarray(cos_thf, np.float32)
+    sn = np.ascontiguousarray(sin_thf, np.float32)
+    assert y.shape[1] == D and cs.shape == (y.shape[0], H, 64) == sn.shape
+    lib(real).orc_rope_apply(y.ctypes.data, y.shape[0], cs.ctypes.data, sn.ctypes.data)
+    return y
+
+
+def gelu(x, real: str = "f64"):
+    """Tensor.gelu, tanh form (ltx/block.zig:332), elementwise."""
+    dt = _rdt(real)
+    x = np.ascontiguousarray(x, dt)
+    y = np.empty_like(x)
+    lib(real).orc_gelu(x.ctypes.data, x.size, y.ctypes.data)
     return y
 
 

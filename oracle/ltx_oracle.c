@@ -654,3 +654,12 @@ void orc_linear(const real* x, int M, int K, const uint16_t* wbf, const int8_t* 
 void orc_rms(const real* x, int M, int N, const uint16_t* w, real* y) { rms_rows(x, M, N, w, y); }
 
 int orc_real_size(void) { return (int)sizeof(real); }
+
+/* Isolated split-half RoPE application, in place on x [T][4096] with cos/sin
+ * in graph layout [T][32][64] (ltx/block.zig:69-77). */
+void orc_rope_apply(real* x, int T, const float* cs, const float* sn) { rope_apply(x, T, cs, sn); }
+
+/* Isolated GELU, tanh form (ltx/block.zig:332), elementwise over n values. */
+void orc_gelu(const real* x, long n, real* y) {
+    for (long i = 0; i < n; i++) y[i] = gelu_tanh(x[i]);
+}

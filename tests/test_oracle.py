@@ -312,3 +312,188 @@ def test_closed_form_catches_planted_mistakes(special, mistake):
     assert oracle.rel_rms(out, want) < 1e-12
     assert oracle.rel_rms(oracle.block_np(bt, inp, c, s), want) < 1e-12
     assert oracle.rel_rms(oracle.block_np(bt, inp, c, s, mistake=mistake), want) > 4e-3
+
+
+# ---- RMSNorm, GELU-tanh and the RoPE application ---------------------------
+# Pinned by library routines (torch f64) and by invariants of the rotation,
+# not by restating the oracle's own expressions. Each check is also run on a
+# numpy variant with a planted mistake, which it must reject.
+
+def _bf16_bits(a):
+    return (np.asarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def _rms_rows_input():
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((6, D)) * rng.uniform(0.05, 50.0, (6, 1))
+    x[0] *= 1e-4  # mean(x^2) ~ 1e-8 < eps: the eps placement decides this row
+    x[1, ::7] += 40.0  # outliers
+    return x
+
+
+def _torch_rms(x, w_bits=None):
+    import torch
+    import torch.nn.functional as F
+    w = None if w_bits is None else torch.from_numpy(
+        (w_bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64))
+    return F.rms_norm(torch.from_numpy(x), (D,), weight=w, eps=1e-6).numpy()
+
+
+D = oracle.D
+
+
+def test_rms_matches_torch_rms_norm():
+    """rmsNoW / rmsW (ltx/block.zig:28-34, ZML nn.rmsNorm with eps 1e-6 and
+    the norm weight applied after) against torch.nn.functional.rms_norm."""
+    x = _rms_rows_input()
+    w = _bf16_bits(np.random.default_rng(12).standard_normal(D))
+    for wb in (None, w):
+        got, want = oracle.rms(x, wb), _torch_rms(x, wb)
+        assert np.abs(got - want).max() <= 1e-14 * np.abs(want).max(), wb is None
+
+
+@pytest.mark.parametrize("mistake", ["eps_outside", "layernorm", "sum_not_mean"])
+def test_rms_torch_check_catches_planted_mistakes(mistake):
+    x = _rms_rows_input()
+    if mistake == "eps_outside":
+        bad = x / (np.sqrt((x * x).mean(-1, keepdims=True)) + 1e-6)
+    elif mistake == "layernorm":
+        c = x - x.mean(-1, keepdims=True)
+        bad = c / np.sqrt((c * c).mean(-1, keepdims=True) + 1e-6)
+    else:
+        bad = x / np.sqrt((x * x).sum(-1, keepdims=True) + 1e-6)
+    want = _torch_rms(x)
+    assert np.abs(bad - want).max() > 1e-6 * np.abs(want).max()
+
+
+def _gelu_input():
+    x = np.concatenate([np.linspace(-12, 12, 24001), np.array([0.0, -0.0, 1e-300, -1e-300, 30, -30, 1e3, -1e3])])
+    return x
+
+
+def _torch_gelu_tanh(x):
+    import torch
+    import torch.nn.functional as F
+    return F.gelu(torch.from_numpy(x), approximate="tanh").numpy()
+
+
+def test_gelu_matches_torch_tanh_form():
+    """Tensor.gelu (ltx/block.zig:332), the tanh form, against
+    torch.nn.functional.gelu(approximate="tanh") in f64, negative tails
+    included (where 1 + tanh cancels)."""
+    x = _gelu_input()
+    got, want = oracle.gelu(x), _torch_gelu_tanh(x)
+    assert np.all(np.abs(got - want) <= 1e-13 * np.abs(x) + 1e-300)
+    # odd-part identity of any 0.5 x (1 + tanh(odd u)) form, and the limits
+    assert np.abs(got - oracle.gelu(-x) - x).max() <= 1e-12
+    assert oracle.gelu(np.array([0.0]))[0] == 0.0
+    assert oracle.gelu(np.array([-30.0]))[0] == 0.0 and oracle.gelu(np.array([30.0]))[0] == 30.0
+
+
+@pytest.mark.parametrize("mistake", ["erf", "kappa", "sqrt_pi"])
+def test_gelu_torch_check_catches_planted_mistakes(mistake):
+    from scipy.special import erf
+    x = _gelu_input()[:24001]
+    if mistake == "erf":
+        bad = 0.5 * x * (1 + erf(x / np.sqrt(2)))
+    elif mistake == "kappa":
+        bad = 0.5 * x * (1 + np.tanh(np.sqrt(2 / np.pi) * (x + 0.0447 * x ** 3)))
+    else:
+        bad = 0.5 * x * (1 + np.tanh(np.sqrt(1 / np.pi) * (x + 0.044715 * x ** 3)))
+    assert np.abs(bad - _torch_gelu_tanh(x)).max() > 1e-9
+
+
+def _rope_case():
+    grid = reference_probe_grid()
+    cos, sin = oracle.rope_tables(grid)  # bundle layout [H, T, 64]
+    cs, sn = cos.transpose(1, 0, 2).copy(), sin.transpose(1, 0, 2).copy()  # graph layout [T, H, 64]
+    x = np.random.default_rng(13).standard_normal((grid.shape[1], D))
+    return x, cs, sn
+
+
+def _rope_variant(x, cs, sn, mistake):
+    """numpy RoPE with one planted mistake (for the checks' teeth)."""
+    T = x.shape[0]
+    c, s = cs.astype(np.float64), sn.astype(np.float64)
+    if mistake == "interleaved":  # pairs (2f, 2f+1) instead of (f, f+64)
+        x4 = x.reshape(T, oracle.H, 64, 2)
+        a, b = x4[..., 0], x4[..., 1]
+        return np.stack([a * c - b * s, b * c + a * s], -1).reshape(T, D)
+    x4 = x.reshape(T, oracle.H, 2, 64)
+    a, b = x4[:, :, 0], x4[:, :, 1]
+    if mistake == "sign":
+        out = [a * c + b * s, b * c - a * s]
+    elif mistake == "cos_sin_swapped":
+        out = [a * s - b * c, b * s + a * c]
+    elif mistake == "head_slots_shifted":  # head h reads head h+1's slots
+        c, s = np.roll(c, -1, axis=1), np.roll(s, -1, axis=1)
+        out = [a * c - b * s, b * c + a * s]
+    else:
+        raise ValueError(mistake)
+    return np.concatenate(out, -1).reshape(T, D)
+
+
+def _rope_checks(rope, x, cs, sn):
+    """The invariants a split-half RoPE (ltx/block.zig:69-77, reshape to
+    [.., h, p=2, f=64] at ltx/block.zig:220-226) must satisfy; returns the
+    names of the checks that fail."""
+    import torch
+    T = x.shape[0]
+    fails = []
+    y = rope(x, cs, sn)
+    # 1. z = x[h, f] + i x[h, 64 + f] is multiplied by e^{i theta}, cos/sin = the tables (torch complex)
+    x4 = torch.from_numpy(x.reshape(T, oracle.H, 2, 64))
+    z = torch.complex(x4[:, :, 0], x4[:, :, 1])
+    e = torch.complex(torch.from_numpy(cs.astype(np.float64)), torch.from_numpy(sn.astype(np.float64)))
+    r = z * e
+    want = torch.cat([r.real, r.imag], -1).reshape(T, D).numpy()
+    if np.abs(y - want).max() > 1e-14 * np.abs(want).max():
+        fails.append("complex")
+    # 2. head 0's identity slots (tables (1, 0)): dimensions 0, 1, 64, 65 pass unchanged
+    if not np.array_equal(y[:, [0, 1, 64, 65]], x[:, [0, 1, 64, 65]]):
+        fails.append("identity")
+    # 3. each (f, f + 64) pair keeps its 2-norm (cos^2 + sin^2 = 1 to f32 rounding)
+    n0 = x.reshape(T, oracle.H, 2, 64) ** 2
+    n1 = y.reshape(T, oracle.H, 2, 64) ** 2
+    if np.abs(n1.sum(2) - n0.sum(2)).max() > 1e-6 * n0.sum(2).max():
+        fails.append("pair_norm")
+    return fails
+
+
+def test_rope_apply_pinned_by_rotation_invariants():
+    x, cs, sn = _rope_case()
+    assert _rope_checks(oracle.rope_apply, x, cs, sn) == []
+
+
+def test_rope_apply_relative_positions():
+    """On a grid that moves along one axis only, the per-head dot product of
+    a rotated q and a rotated k depends only on the position difference
+    (the angle is linear in the position): q and k read the same slots and
+    cos, sin are of one angle."""
+    for axis in range(3):
+        pos = np.zeros((3, 12), np.float32)
+        step = 1.0 if axis == 0 else 32.0
+        pos[axis] = np.arange(12) * step
+        grid = np.ascontiguousarray(np.stack([pos, pos], -1))
+        cos, sin = oracle.rope_tables(grid)
+        cs, sn = cos.transpose(1, 0, 2).copy(), sin.transpose(1, 0, 2).copy()
+        rng = np.random.default_rng(14 + axis)
+        q = np.repeat(rng.standard_normal((1, D)), 12, 0)
+        k = np.repeat(rng.standard_normal((1, D)), 12, 0)
+        rq, rk = oracle.rope_apply(q, cs, sn), oracle.rope_apply(k, cs, sn)
+        dots = np.einsum("thd,shd->hts", rq.reshape(12, oracle.H, 128), rk.reshape(12, oracle.H, 128))
+        for d in (1, 3, 5):
+            for t in range(12 - d - 2):
+                a, b = dots[:, t, t + 2], dots[:, t + d, t + 2 + d]
+                assert np.abs(a - b).max() <= 1e-5 * np.abs(dots).max(), (axis, d, t)
+        # a shift that changes the difference does change the products
+        assert np.abs(dots[:, 0, 2] - dots[:, 0, 5]).max() > 1e-3 * np.abs(dots).max()
+
+
+@pytest.mark.parametrize("mistake", ["interleaved", "sign", "cos_sin_swapped", "head_slots_shifted"])
+def test_rope_checks_catch_planted_mistakes(mistake):
+    x, cs, sn = _rope_case()
+    fails = _rope_checks(lambda a, c, s: _rope_variant(a, c, s, mistake), x, cs, sn)
+    assert fails, mistake
+    if mistake == "interleaved":
+        assert "identity" in fails and "pair_norm" in fails
