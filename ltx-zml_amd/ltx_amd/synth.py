@@ -60,6 +60,42 @@ def make_block(block: int = 0, seed: int = 1, dist: str = "t3", std: float = 0.0
     return bt
 
 
+_ZERO_BF16 = {}
+
+
+def make_block_q8(block: int, seed: int = 3, scale_dtype: str = "F16") -> bf.BlockTensors:
+    """A seeded block whose seven projections are int8 from the start: q
+    uniform over [-127, 127] and one scale per group of 128 drawn as
+    0.02 / std(q) x U(0.5, 1.5) (weights of std ~0.02, the magnitude of
+    make_block's), rounded to the scale type. The small tensors (biases,
+    norm and gate weights, sst, psst) are drawn as in make_block with
+    N(0, 1). The bf16 tensors of the int8 projections are never read when
+    the int8 companions are present (neither by the upload nor by the
+    oracle); they share one read-only zero array. About 0.5 s a block,
+    against ~40 s for quantising drawn weights, which is what lets a test
+    hold 48 independently seeded blocks."""
+    base = {}
+    q8, q8s = {}, {}
+    qbase = set(bf.Q8_BASE.values())
+    for field, _, shape, _ in bf.BASE_SPECS:
+        if field in qbase:
+            if shape not in _ZERO_BF16:
+                z = np.zeros(shape, np.uint16)
+                z.setflags(write=False)
+                _ZERO_BF16[shape] = z
+            base[field] = _ZERO_BF16[shape]
+        else:
+            base[field] = _tensor(block, seed, field, shape, "normal", 0.02)
+    qstd = np.float32(np.sqrt((255 ** 2 - 1) / 12.0))  # std of the uniform integers -127..127
+    for qn, field in bf.Q8_BASE.items():
+        O, I = dict((s[0], s[2]) for s in bf.BASE_SPECS)[field]
+        g = rng(seed, f"{block}:{qn}:q8")
+        q8[qn] = g.integers(-127, 128, size=(O, I), dtype=np.int8)
+        sc = (np.float32(0.02) / qstd) * g.uniform(0.5, 1.5, size=(O, I // bf.GROUP)).astype(np.float32)
+        q8s[qn] = sc.astype(np.float16) if scale_dtype == "F16" else sc
+    return bf.BlockTensors(block, base, q8, q8s)
+
+
 def latent_grid(frames: int, height: int, width: int) -> np.ndarray:
     """[3, T, 2] f32 (start, end) positions, tokens frame-major. Positions are
     integers so the f32 grid is exact: frame index, and pixel coordinates

@@ -272,12 +272,63 @@ static real* weight_t(const uint16_t* wbf, const int8_t* q, const void* s, int s
     return wt;
 }
 
+/* Few rows (M <= SMALL_M): the weight is dequantised panel by panel (NP
+ * columns x KC k at a time) into a per-thread buffer and multiplied with the
+ * same micro-kernels; the whole transposed weight (and the page faults of
+ * allocating it per call) is never built. Each output is still one chain of
+ * fused multiply-adds over k in ascending order from 0, the accumulator
+ * passing through C between k-blocks unchanged, so the result is bit-identical
+ * to gemm_kn's for every row. */
+#define SMALL_M 256
+#define NP 64
+static void linear_small(const real* x, int M, int K, const uint16_t* wbf, const int8_t* q, const void* s,
+                         int scale_f16, int N, real* y) {
+    const int G = K / 128;
+#pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; m++) memset(y + (size_t)m * N, 0, sizeof(real) * (size_t)N);
+#pragma omp parallel
+    {
+        real* pan = (real*)malloc(sizeof(real) * (size_t)KC * NP);
+#pragma omp for schedule(dynamic, 1)
+        for (int n0 = 0; n0 < N; n0 += NP) {
+            const int np = N - n0 < NP ? N - n0 : NP;
+            for (int k0 = 0; k0 < K; k0 += KC) {
+                const int kc = K - k0 < KC ? K - k0 : KC;
+                for (int j = 0; j < np; j++) {
+                    const size_t n = (size_t)(n0 + j);
+                    for (int k = 0; k < kc; k++) {
+                        const size_t kk = (size_t)(k0 + k);
+                        real v;
+                        if (q) {
+                            float sc = scale_f16 ? f16_to_f32(((const uint16_t*)s)[n * G + kk / 128])
+                                                 : ((const float*)s)[n * G + kk / 128];
+                            v = (real)((float)q[n * K + kk] * sc);
+                        } else {
+                            v = bfr(wbf, n * K + kk);
+                        }
+                        pan[(size_t)k * NP + j] = v;
+                    }
+                }
+                for (int m = 0; m < M; m += MR)
+                    for (int j = 0; j < np; j += NR)
+                        gemm_micro(x + (size_t)m * K + k0, K, pan + j, NP, y + (size_t)m * N + n0 + j, N,
+                                   M - m < MR ? M - m : MR, np - j < NR ? np - j : NR, kc);
+            }
+        }
+        free(pan);
+    }
+}
+
 /* lin / linQ (ltx/block.zig:22-26, 473-477): y = x W^T (+ b) */
 static void linear(const real* x, int M, int K, const uint16_t* wbf, const int8_t* q, const void* s,
                    int scale_f16, const uint16_t* b, int N, real* y) {
-    real* wt = weight_t(wbf, q, s, scale_f16, N, K);
-    gemm_kn(x, M, K, wt, N, y);
-    free(wt);
+    if (M <= SMALL_M) {
+        linear_small(x, M, K, wbf, q, s, scale_f16, N, y);
+    } else {
+        real* wt = weight_t(wbf, q, s, scale_f16, N, K);
+        gemm_kn(x, M, K, wt, N, y);
+        free(wt);
+    }
     if (b) {
 #pragma omp parallel for schedule(static)
         for (int m = 0; m < M; m++)

@@ -176,3 +176,35 @@ def test_denoise_loop(ctx, core_dev, denoise_case, mode, gate):
     assert np.array_equal(host(dl2).view(np.uint32), stepped.view(np.uint32))
     for w in ws:
         w.free()
+
+
+def test_denoise_velocity_f32_from_oracle_conditioning(ctx, core_np, core_dev, denoise_case):
+    """Mode F32: the first step's velocity computed on the GPU (patchify,
+    both blocks, tail) from the oracle's conditioning tables (ts9r, emb,
+    pts2r in f64, rounded to f32) is within the 1e-5 gate of the oracle's
+    velocity; from the GPU's own f32 sinusoid-fed tables it is not held to
+    it (test_denoise_loop). The excess is the conditioning's: t * 1000 *
+    freq reaches 1,000 rad, where one ulp of an f32 exp or of the phase moves
+    cos and sin by ~1e-5."""
+    c = denoise_case
+    T = 64
+    sig = c["sig"]
+    say("denoise velocity f32 from the oracle's conditioning T=64 blocks=2")
+    t = oracle.sched_timesteps(c["mask"], sig[0])
+    tstab = oracle.core_ts9r(core_np, t).astype(np.float32)
+    emb = oracle.core_emb(core_np, t).astype(np.float32)
+    pts2 = oracle.core_pts2r(core_np, sig[0]).astype(np.float32)
+    want = c["want"][0][0]
+    ws = [ctx.upload(b) for b in c["blocks"]]
+    bufs = [torch.empty((T, 4096), dtype=torch.float32, device="cuda") for _ in range(2)]
+    ctx.patchify(core_dev, dev(c["lat0"]), bufs[0])
+    args = [dev(tstab), dev(c["tidx"]), dev(c["ctx"]), dev(pts2), dev(c["cos"]), dev(c["sin"])]
+    for b, w in enumerate(ws):
+        ctx.forward(w, bufs[b % 2], *args, bufs[(b + 1) % 2], mode=rt.MODES["f32"])
+    vel = torch.empty((T, 128), dtype=torch.float32, device="cuda")
+    ctx.tail(core_dev, bufs[len(ws) % 2], dev(emb), dev(c["tidx"]), vel)
+    r = oracle.rel_rms(host(vel), want)
+    for w in ws:
+        w.free()
+    print(f"velocity from the oracle's conditioning: rel-RMS {r:.3e}", flush=True)
+    assert r <= 1e-5

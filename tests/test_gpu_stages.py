@@ -10,11 +10,16 @@ dilute an error in one of them:
   cross-attention branch x_ca - x_sa   (s5CaOut)
   FFN branch             y - x_ca      (s7FfOut * ada5)
 
-Gates (rel-RMS): fp16 operands 2e-3, f32 1e-5 per stage. bf16 operands are
-printed and held to 1.5e-2: one bf16 rounding of a value has a relative RMS
-error of about 2^-9 / sqrt(3) = 1.1e-3, and each stage rounds its inputs and
-weights, so bf16 stages sit at 2-8e-3 and the 2e-3 stage gate is out of reach
-by construction (fp16 carries 3 more mantissa bits).
+Gates (rel-RMS): fp16 operands 2e-3, f32 1e-5 per stage. bf16 operands: the
+block output 2e-3, the stages printed and held to 1.5e-2. One bf16 rounding
+of a value has a relative RMS error of about 2^-9 / sqrt(3) = 1.1e-3, and a
+branch sums several: in an f64 simulation of this pipeline's rounding points
+at T = 256 (the GPU's bf16 numbers reproduce within 5 %), rounding only the
+modulated norms that feed the GEMMs puts the self-attention branch at
+2.5e-3, rounding only the dequantised weights at 2.5e-3 too, and every
+rounding together at 5.0e-3 (the block output 1.9e-3). The per-stage 2e-3
+gate is out of reach with bf16 MFMA operands by construction; fp16 carries
+3 more mantissa bits (the same simulation: 6.3e-4).
 
 Also here: the closed-form special case (tests/blockcases.py) on the GPU,
 which pins the AdaLN row order, the K/V modulation and the 2 sigmoid gate
@@ -120,6 +125,8 @@ def test_block_stages(ctx, block0, mode, T, S):
     say("  " + " ".join(f"{k}={v:.2e}" for k, v in r.items()))
     bad = {k: v for k, v in r.items() if not v <= GATE[mode]}
     assert not bad, f"stages over the {GATE[mode]:.0e} gate: {bad}"
+    if mode == "bf16":
+        assert r["y"] <= 2e-3, r
 
 
 @pytest.mark.parametrize("T,S", [(256, 64), (2048, 64)])

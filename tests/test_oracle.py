@@ -497,3 +497,20 @@ def test_rope_checks_catch_planted_mistakes(mistake):
     assert fails, mistake
     if mistake == "interleaved":
         assert "identity" in fails and "pair_norm" in fails
+
+
+def test_linear_small_and_blocked_paths_agree_bitwise(block0):
+    """The oracle's GEMM takes a panel path for up to 256 rows and a blocked
+    path above; both chain each output's fused multiply-adds over k in
+    ascending order, so a row's result does not depend on the path (int8
+    with f32 scales, int8 with f16 scales, bf16 weights with a bias)."""
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((300, D))
+    q, s = block0.q8["f1"][:640], block0.q8s["f1"][:640]
+    cases = [dict(q=q, s=s), dict(q=q, s=s.astype(np.float16)),
+             dict(w_bf16=block0.base["q1_w"][:600], b_bf16=block0.base["q1_b"][:600])]
+    for kw in cases:
+        big = oracle.linear(x, **kw)
+        for rows in (slice(0, 64), slice(37, 293)):
+            small = oracle.linear(x[rows], **kw)
+            assert np.array_equal(small.view(np.uint64), big[rows].view(np.uint64))
