@@ -157,7 +157,7 @@ void ltx_block_graph_destroy(ltx_block_graph* g);
  * last call did not produce reads NULL / 0. */
 enum {
     LTX_ST_NORM_MSA,    /* s1NormMsa: modulated norm, operand dtype [T][4096] */
-    LTX_ST_Q1,          /* normed+roped q times log2(e)/sqrt(128), head-major [32][T][128] (f32 mode: [T][4096], unscaled) */
+    LTX_ST_Q1,          /* normed+roped q times log2(e)/sqrt(128), [T][4096] (f32 mode: unscaled) */
     LTX_ST_K1,          /* normed+roped k, same layout */
     LTX_ST_V1,          /* v: [32][128][T] (f32 mode: [T][4096]) */
     LTX_ST_GLOG1,       /* gate logits [T][32] f32 */
@@ -169,8 +169,8 @@ enum {
     LTX_ST_FF_IN,       /* s6FfIn [T][4096] */
     LTX_ST_FF_H,        /* gelu(ff1) [T][16384] */
     LTX_ST_GLOG2,       /* cross-attention gate logits [T][32] f32 */
-    LTX_ST_Q2,          /* normed cross q times log2(e)/sqrt(128), [32][T][128] (f32 mode: [T][4096], unscaled) */
-    LTX_ST_K2,          /* normed cross k [32][S][128] (f32 mode: [S][4096]) */
+    LTX_ST_Q2,          /* normed cross q times log2(e)/sqrt(128), [T][4096] (f32 mode: unscaled) */
+    LTX_ST_K2,          /* normed cross k [S][4096] */
     LTX_ST_V2,          /* cross v: [32][128][S] (f32 mode: [S][4096]) */
     LTX_ST_VELOCITY,    /* ltx_denoise: the last step's velocity [T][128] f32 */
     LTX_ST_COUNT

@@ -242,13 +242,19 @@ static void qknorm16(ltx_ctx* c, int mode, const void* x, int ldx, const void* w
 }
 
 // q_scaled: Q already carries kAttnC (the block path); else plain Q.
+// qk_rows: Q and K as token rows [L][4096] (the block's qk-norm output);
+// else head-major [32][L][128] (ltx_op_attention).
 static void attn16(ltx_ctx* c, int mode, const void* q, const void* k, const void* vt, const float* glog, void* out,
                    int lq, int lkv, bool q_scaled, hipStream_t st, const char* label = nullptr,
-                   unsigned long long* sat = nullptr) {
+                   unsigned long long* sat = nullptr, bool qk_rows = false) {
     LtxAttnArgs a{};
     a.sat = sat;
     a.q = q;
     a.k = k;
+    a.q_hs = qk_rows ? LTX_HD : lq * LTX_HD;
+    a.q_rs = qk_rows ? LTX_D : LTX_HD;
+    a.k_hs = qk_rows ? LTX_HD : lkv * LTX_HD;
+    a.k_rs = qk_rows ? LTX_D : LTX_HD;
     a.vt = vt;
     a.glog = glog;
     a.out = out;
@@ -425,7 +431,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
         c->launch(mode == LTX_MODE_BF16 ? "ltx_qknorm2_bf16" : "ltx_qknorm2_f16", T, 1, 1, 256, &qa, st);
     }
     stream_after(st, sd, c->side_ev[1]);
-    attn16(c, mode, b.qh1, b.kh1, b.vt1, (const float*)b.glog1, b.o1, T, T, true, st, "attn:self", sat);
+    attn16(c, mode, b.qh1, b.kh1, b.vt1, (const float*)b.glog1, b.o1, T, T, true, st, "attn:self", sat, true);
     g = LtxGemmArgs{};
     g.out = b.x_sa;
     g.resid = x;
@@ -464,7 +470,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
         qknorm16(c, mode, b.q2_16, LTX_D, w->qn2.p, nullptr, nullptr, b.qh2, T, kAttnC, st);
         qknorm16(c, mode, b.k2_16, LTX_D, w->kn2.p, nullptr, nullptr, b.kh2, S, 1.0f, st);
         stream_after(st, sd, c->side_ev[3]);  // glog2 ready
-        attn16(c, mode, b.qh2, b.kh2, b.vt2, (const float*)b.glog2, b.o2, T, S, true, st, "attn:cross", sat);
+        attn16(c, mode, b.qh2, b.kh2, b.vt2, (const float*)b.glog2, b.o2, T, S, true, st, "attn:cross", sat, true);
     }
     g = LtxGemmArgs{};
     g.out = b.x_ca;

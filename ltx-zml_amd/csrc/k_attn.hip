@@ -51,8 +51,8 @@ __device__ void attn_body(const LtxAttnArgs& a) {
     const int q0 = qt * QT + w * QW;
     const int lq = a.lq, lkv = a.lkv;
 
-    const uint16_t* Q = (const uint16_t*)a.q + (size_t)h * lq * LTX_HD;
-    const uint16_t* K = (const uint16_t*)a.k + (size_t)h * lkv * LTX_HD;
+    const uint16_t* Q = (const uint16_t*)a.q + (size_t)h * a.q_hs;
+    const uint16_t* K = (const uint16_t*)a.k + (size_t)h * a.k_hs;
     const uint16_t* V = (const uint16_t*)a.vt + (size_t)h * LTX_HD * lkv;
 
     // Q^T operand: lane holds Q[q][16 c + 8 (lane / 32) .. + 8] for its query.
@@ -63,7 +63,7 @@ __device__ void attn_body(const LtxAttnArgs& a) {
         const int q = min(q0 + 32 * qb + fr, lq - 1);
 #pragma unroll
         for (int c = 0; c < 8; c++)
-            qf[qb][c] = __builtin_bit_cast(v8, *(const u32x4*)(Q + (size_t)q * LTX_HD + 16 * c + 8 * hi));
+            qf[qb][c] = __builtin_bit_cast(v8, *(const u32x4*)(Q + (size_t)q * a.q_rs + 16 * c + 8 * hi));
     }
 
     f32x16 o[QB][4];
@@ -86,7 +86,7 @@ __device__ void attn_body(const LtxAttnArgs& a) {
         for (int i = 0; i < NCH; i++) {
             int id = tid + NT * i, row = id >> 4, c16 = id & 15;
             int key = FULL ? kv0 + row : min(kv0 + row, lkv - 1);
-            rk[i] = *(const u32x4*)(K + (size_t)key * LTX_HD + 8 * c16);
+            rk[i] = *(const u32x4*)(K + (size_t)key * a.k_rs + 8 * c16);
         }
 #pragma unroll
         for (int i = 0; i < NCH; i++) {
@@ -353,6 +353,7 @@ struct AttnPP {
     const LtxAttnArgs& a;
     __amdgpu_buffer_rsrc_t rk, rv;
     uint32_t gk[2], gv[2];  // per-lane DMA source offsets in tile 0
+    uint32_t kr;            // bytes between consecutive K rows
     int lw;                 // this wave's 2 KB slice of a stage
     uint32_t ok[4];         // K fragment offsets per 32-dim step ks (kb adds 4096)
     uint32_t ov[2];         // V^T fragment offsets per 32-key step kc (db adds 2048)
@@ -360,6 +361,7 @@ struct AttnPP {
     f32x4 o[8][2];          // O^T [db][qb]
     f32x4 s[4][2];          // S^T [kb][qb]
     v8 pf[2][2];            // P^T operand [kc][qb]
+    v8 vpre[4];             // V^T fragments kc = 0, db = 0..3 of the next PV, read in the softmax phase (resident form)
     f32x4 sb[2];            // -m of the lane's query in block qb: the S MFMAs start from it
     f32x2 m, l;             // running max and partial sum per query block (vectors, not arrays: kept in registers)
     float C;
@@ -378,7 +380,7 @@ struct AttnPP {
 #pragma unroll
             for (int i = 0; i < 2; i++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (attn_lds_ptr)(d + 8192 * h + 1024 * i), 16, gk[i],
-                                                         t * 16384 + 8192 * h, 0, 0);
+                                                         (uint32_t)(64 * t + 32 * h) * kr, 0, 0);
     }
     template <int S>
     __device__ __forceinline__ void dma_v(int t) {
@@ -392,14 +394,21 @@ struct AttnPP {
     }
 
     // MFMA phase t: PV(t-1) from the V^T tile at sv, then S(t) from the K tile
-    // at sk; each fragment feeds the MFMAs of both query blocks
+    // at sk; each fragment feeds the MFMAs of both query blocks. PRE: the
+    // first four V^T fragments were read into vpre at the end of the softmax
+    // phase before (prefetch_v), so the phase opens with MFMAs instead of
+    // waiting out its first LDS reads (the resident form: its K/V never
+    // change, so any phase may read them).
+    template <bool PRE = false>
     __device__ __forceinline__ void mfma_phase(const uint8_t* sk, const uint8_t* sv, bool ds, bool dp) {
         if (dp) {
 #pragma unroll
             for (int kc = 0; kc < 2; kc++)
 #pragma unroll
                 for (int db = 0; db < 8; db++) {
-                    const v8 vf = __builtin_bit_cast(v8, *(const u32x4*)(sv + ov[kc] + 2048 * db));
+                    const v8 vf = PRE && kc == 0 && db < 4
+                                      ? vpre[db & 3]
+                                      : __builtin_bit_cast(v8, *(const u32x4*)(sv + ov[kc] + 2048 * db));
                     o[db][0] = Op<T>::mfma16(vf, pf[kc][0], o[db][0]);
                     o[db][1] = Op<T>::mfma16(vf, pf[kc][1], o[db][1]);
                 }
@@ -420,13 +429,19 @@ struct AttnPP {
                 }
         }
         // fragment reads eight MFMAs (four reads) ahead (masks: 0x100 DS
-        // read, 0x008 MFMA)
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        // read, 0x008 MFMA); with PRE the first four are already in registers
+        if (!PRE) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
         for (int i = 0; i < 32; i++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
             if (i < 28) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
+    }
+
+    // the first four V^T fragments of the next MFMA phase's PV (tile at sv)
+    __device__ __forceinline__ void prefetch_v(const uint8_t* sv) {
+#pragma unroll
+        for (int db = 0; db < 4; db++) vpre[db] = __builtin_bit_cast(v8, *(const u32x4*)(sv + ov[0] + 2048 * db));
     }
 
     // P^T operands and their row sums, per query block. s holds score - m
@@ -542,8 +557,10 @@ struct AttnPP {
         const int lkv = a.lkv;
         nt = lkv / 64;
         C = a.scale_log2;
-        rk = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint16_t*)a.k + (size_t)h * lkv * LTX_HD), 0,
-                                               lkv * LTX_HD * 2, ASP_RSRC_W3);
+        // K rows are kr bytes apart (head-major: 256; token rows: 8 KB)
+        kr = 2u * (uint32_t)a.k_rs;
+        rk = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint16_t*)a.k + (size_t)h * a.k_hs), 0,
+                                               (int)((uint32_t)(lkv - 1) * kr + 2u * LTX_HD), ASP_RSRC_W3);
         rv = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint16_t*)a.vt + (size_t)h * LTX_HD * lkv), 0,
                                                lkv * LTX_HD * 2, ASP_RSRC_W3);
         lw = 2048 * w;
@@ -555,7 +572,7 @@ struct AttnPP {
             const int r = 4 * (2 * w + i) + (lane >> 4);  // LDS row within the first 32
             const int key = (r & 3) | ((r & 16) >> 2) | ((r & 4) << 1) | ((r & 8) << 1);
             const int c = (lane & 15) ^ (r & 15);
-            gk[i] = (uint32_t)key * 256u + 16u * c;
+            gk[i] = (uint32_t)key * kr + 16u * c;
             const int d = 8 * (2 * w + i) + (lane >> 3);
             const int cv = (lane & 7) ^ ((d >> 1) & 7);
             gv[i] = (uint32_t)d * (uint32_t)lkv * 2u + 16u * cv;
@@ -570,14 +587,14 @@ struct AttnPP {
     // Q^T operands of the wave's queries q0 .. q0 + 31 of head h (rows past
     // lq read row lq - 1)
     __device__ __forceinline__ void load_q(v8 (&dst)[2][4], int h, int q0, int lane) const {
-        const uint16_t* Q = (const uint16_t*)a.q + (size_t)h * a.lq * LTX_HD;
+        const uint16_t* Q = (const uint16_t*)a.q + (size_t)h * a.q_hs;
         const int j = lane >> 4, r = lane & 15;
 #pragma unroll
         for (int qb = 0; qb < 2; qb++) {
             const int q = min(q0 + 16 * qb + r, a.lq - 1);
 #pragma unroll
             for (int ks = 0; ks < 4; ks++)
-                dst[qb][ks] = __builtin_bit_cast(v8, *(const u32x4*)(Q + (size_t)q * LTX_HD + 32 * ks + 8 * j));
+                dst[qb][ks] = __builtin_bit_cast(v8, *(const u32x4*)(Q + (size_t)q * a.q_rs + 32 * ks + 8 * j));
         }
     }
 
@@ -696,6 +713,13 @@ struct AttnPP {
         asm volatile("" ::"v"(sb[0]), "v"(sb[1]));
     }
 
+    // as pin_softmax, and the prefetched V^T fragments of the next PV
+    __device__ __forceinline__ void pin_softmax_pre() {
+        pin_softmax();
+#pragma unroll
+        for (int db = 0; db < 4; db++) asm volatile("" ::"v"(__builtin_bit_cast(u32x4, vpre[db])));
+    }
+
     // after the last softmax of a query tile: the next MFMA phase starts the
     // next tile (S(0) from a zero max, with its Q)
     __device__ __forceinline__ void next_tile(const v8 (&qn)[2][4]) {
@@ -707,9 +731,10 @@ struct AttnPP {
             for (int ks = 0; ks < 4; ks++) qf[qb][ks] = qn[qb][ks];
     }
 
+    template <bool PRE>
     __device__ __forceinline__ void rphase(const uint8_t* sk, const uint8_t* sv, bool ds, bool dp) {
         __builtin_amdgcn_s_setprio(1);
-        mfma_phase(sk, sv, ds, dp);
+        mfma_phase<PRE>(sk, sv, ds, dp);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
         barrier();
@@ -743,7 +768,7 @@ struct AttnPP {
                     for (int i = 0; i < 2; i++) {
                         __builtin_amdgcn_raw_ptr_buffer_load_lds(
                             rk, (attn_lds_ptr)(kres + 16384 * t + lw + 8192 * hh + 1024 * i), 16, gk[i],
-                            t * 16384 + 8192 * hh, 0, 0);
+                            (uint32_t)(64 * t + 32 * hh) * kr, 0, 0);
                         __builtin_amdgcn_raw_ptr_buffer_load_lds(
                             rv, (attn_lds_ptr)(vres + 16384 * t + lw + 8192 * hh + 1024 * i), 16, gv[i],
                             t * 128 + 128 * a.lkv * hh, 0, 0);
@@ -766,7 +791,10 @@ struct AttnPP {
             // t = 0: PV of the previous tile's last key tile, S(0); then the
             // previous tile's output, this tile's gate logits and the next
             // tile's Q (read at t = nt - 1)
-            rphase(kres, vres + 16384 * (nt - 1), true, prev);
+            if (prev)
+                rphase<true>(kres, vres + 16384 * (nt - 1), true, true);
+            else
+                rphase<false>(kres, vres + 16384 * (nt - 1), true, false);
             // unconditional (rows past lq read row lq - 1), so that every
             // path waits for these loads where qf takes them; issued before
             // the output stores, which would otherwise queue ahead of them
@@ -777,25 +805,28 @@ struct AttnPP {
             }
             softmax(true);
             if (nt == 1) next_tile(qn);
-            pin_softmax();
+            prefetch_v(vres);
+            pin_softmax_pre();
             barrier();
             for (int t = 1; t < nt - 1; t++) {
-                rphase(kres + 16384 * t, vres + 16384 * (t - 1), true, true);
+                rphase<true>(kres + 16384 * t, vres + 16384 * (t - 1), true, true);
                 softmax(false);
-                pin_softmax();
+                prefetch_v(vres + 16384 * t);
+                pin_softmax_pre();
                 barrier();
             }
             if (nt > 1) {
-                rphase(kres + 16384 * (nt - 1), vres + 16384 * (nt - 2), true, true);
+                rphase<true>(kres + 16384 * (nt - 1), vres + 16384 * (nt - 2), true, true);
                 softmax(false);
                 next_tile(qn);
-                pin_softmax();
+                prefetch_v(vres + 16384 * (nt - 1));
+                pin_softmax_pre();
                 barrier();
             }
             q0 += 256 * wph;
         }
         // the last tile's last PV, then its output
-        rphase(kres, vres + 16384 * (nt - 1), false, true);
+        rphase<true>(kres, vres + 16384 * (nt - 1), false, true);
         store_out<32>(patch, h, q0 - 256 * wph, lane, gl, bad);
         if (g == 0) __builtin_amdgcn_s_barrier();
         range_report(a.sat, bad);

@@ -90,13 +90,14 @@ typedef struct {
 } LtxGemmArgs;
 
 // Full-row qk RMSNorm (weighted, over all 4096 channels) + optional split-half
-// RoPE, writing the head-major 16-bit layout [H][rows][HD] the attention reads.
+// RoPE, writing 16-bit rows [rows][D] (head h at columns h * HD ..), the
+// layout of its input: every token's output is one contiguous 8 KB row.
 typedef struct {
     const void* x;      // [rows][ldx] pre-norm projections, in the 16-bit operand type
     const float* w;     // [D] norm weight (f32 copy of the bf16 tensor)
     const float* cos;   // [rows][H][64] or NULL (no RoPE)
     const float* sin;
-    void* y;            // [H][rows][HD]
+    void* y;            // [rows][D]
     int rows;
     int ldx;
     float oscale;       // applied before the 16-bit rounding (1, or the attention's exponent scale for Q)
@@ -111,7 +112,7 @@ typedef struct {
     const float* wk;
     const float* cos;   // [rows][H][64]
     const float* sin;
-    void* yq;           // [H][rows][HD]
+    void* yq;           // [rows][D]
     void* yk;
     int rows;
     int ldx;
@@ -120,8 +121,10 @@ typedef struct {
 } LtxQkNorm2Args;
 
 // Blockwise online-softmax attention with per-(token, head) gate.
-// q, k: [H][L][HD] 16-bit; vt: [H][HD][Lkv] 16-bit; glog: [Lq][H] f32 gate
-// logits (gate = 2*sigmoid); out: [Lq][D] 16-bit merged heads.
+// q, k: 16-bit, element (h, l, d) at h * hs + l * rs + d: head-major
+// [H][L][HD] (hs = L HD, rs = HD) or token rows [L][D] (hs = HD, rs = D);
+// vt: [H][HD][Lkv] 16-bit; glog: [Lq][H] f32 gate logits (gate =
+// 2*sigmoid); out: [Lq][D] 16-bit merged heads.
 typedef struct {
     const void* q;
     const void* k;
@@ -129,6 +132,8 @@ typedef struct {
     const float* glog;
     void* out;
     int lq, lkv;
+    int q_hs, q_rs;     // element strides of q: head, row
+    int k_hs, k_rs;     // of k
     float scale_log2;   // softmax scale * log2(e)
     int q_tiles;        // ceil(lq / q-tile)
     unsigned long long* sat;  // range guard counter of the 16-bit output or NULL

@@ -92,8 +92,8 @@ def test_full_size_block(ctx, request, mode, scales):
     # stages of this forward (rows picked on the device)
     rows = np.linspace(0, T - 1, 64).astype(np.int64)
     frows = np.linspace(3, T - 5, 32).astype(np.int64)
-    q = _stage(ctx, "q1", dt, (32, T, 128)) / rt.ATTN_C
-    k = _stage(ctx, "k1", dt, (32, T, 128))
+    q = (_stage(ctx, "q1", dt, (T, 32, 128)) / rt.ATTN_C).transpose(1, 0, 2)
+    k = _stage(ctx, "k1", dt, (T, 32, 128)).transpose(1, 0, 2)
     vt = _stage(ctx, "v1", dt, (32, 128, T))
     glog = _stage(ctx, "glog1", torch.float32, (T, 32), rows)
     att = _stage(ctx, "attn1", dt, (T, 4096), rows)

@@ -79,7 +79,7 @@ def gpu_stages(ctx, mode, T, S):
             g[n] = stage(ctx, n, f32, (rows, D))
     else:
         for n, rows, sc in (("q1", T, rt.ATTN_C), ("k1", T, 1.0), ("q2", T, rt.ATTN_C), ("k2", S, 1.0)):
-            g[n] = (stage(ctx, n, dt, (H, rows, HD)) / sc).transpose(1, 0, 2).reshape(rows, D)
+            g[n] = stage(ctx, n, dt, (rows, D)) / sc
         for n, rows in (("v1", T), ("v2", S)):
             g[n] = stage(ctx, n, dt, (H, HD, rows)).transpose(2, 0, 1).reshape(rows, D)
     return g
