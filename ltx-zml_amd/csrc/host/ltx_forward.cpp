@@ -135,9 +135,11 @@ static unsigned long long* sat_of(ltx_ctx* c, int mode) {
     return mode == LTX_MODE_F32 ? nullptr : (unsigned long long*)c->range_ctr.p;
 }
 
+// sat_add: a device count the kernel adds to the range guard (the weights'
+// f16_over in mode F16), or NULL.
 static void norm_mod(ltx_ctx* c, int mode, const float* x, void* y, LtxAda ada, int rows, int ish, int isc,
-                     hipStream_t st) {
-    LtxNormArgs a{x, y, ada, rows, ish, isc, sat_of(c, mode)};
+                     hipStream_t st, const unsigned long long* sat_add = nullptr) {
+    LtxNormArgs a{x, y, ada, rows, ish, isc, sat_of(c, mode), sat_add};
     const char* k = mode == LTX_MODE_F32 ? "ltx_norm_mod_f32" : mode == LTX_MODE_BF16 ? "ltx_norm_mod_bf16" : "ltx_norm_mod_f16";
     c->launch(k, (rows + 3) / 4, 1, 1, 256, &a, st);  // four rows per workgroup (NORM_ROWS)
 }
@@ -358,7 +360,8 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
         Ws32 b;
         carve32(cv, b, T, S);
         // self-attention (ltx/block.zig:546-547, qAttn1 520-530)
-        norm_mod(c, mode, x, b.n_msa, ada, T, 0, 1, st);
+        norm_mod(c, mode, x, b.n_msa, ada, T, 0, 1, st,
+             mode == LTX_MODE_F16 ? (const unsigned long long*)w->f16_over.p : nullptr);
         gemm32(c, w->qkv1, 0, LTX_D, (const float*)b.n_msa, T, (float*)b.q, LTX_EPI_STORE, nullptr, ada, 0, 0, st, "gemm:qkv1");
         gemm32(c, w->qkv1, LTX_D, LTX_D, (const float*)b.n_msa, T, (float*)b.k, LTX_EPI_STORE, nullptr, ada, 0, 0, st, "gemm:qkv1");
         gemm32(c, w->qkv1, 2 * LTX_D, LTX_D, (const float*)b.n_msa, T, (float*)b.v, LTX_EPI_STORE, nullptr, ada, 0, 0, st, "gemm:qkv1");
@@ -409,7 +412,8 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     Ws16 b;
     carve16(cv, b, T, S, c->num_cu);
     // self-attention: n = modulate(rms(x), ada1, ada0); fused q|k|v GEMM
-    norm_mod(c, mode, x, b.n_msa, ada, T, 0, 1, st);
+    norm_mod(c, mode, x, b.n_msa, ada, T, 0, 1, st,
+             mode == LTX_MODE_F16 ? (const unsigned long long*)w->f16_over.p : nullptr);
     LtxGemmArgs g{};
     g.out = b.qk16;
     g.out2 = b.vt1;
@@ -424,6 +428,11 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     // would slow as much as it gains.
     hipStream_t sd = c->side;
     stream_after(sd, st, c->side_ev[0]);
+    if (fail_in_capture()) {
+        hipStreamCaptureStatus cst = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cst) == hipSuccess && cst == hipStreamCaptureStatusActive)
+            throw Error("injected failure inside a graph capture, after the second stream joined it [LTX_FAIL_CAPTURE]");
+    }
     gate16(c, mode, w->g1, b.n_msa, T, (float*)b.glog1, sd);
     {  // q and k norms + RoPE in one pass (the RoPE rows read once)
         LtxQkNorm2Args qa{b.qk16, (const float*)w->qn1.p, (const float*)w->kn1.p, cs, sn, b.qh1, b.kh1,
@@ -524,11 +533,15 @@ bool linear_q8_needs_scratch(const ltx_ctx* c, int N, int K, int mode) {
 // ltx_op_linear_q8 / _noalloc: in the 16-bit modes with the LDS-DMA kernel the
 // weights are first laid out as bytes q + 128 in sc.q and the scales as words
 // [K/128][N] in sc.pairs (both written whole before the GEMM reads them).
+void check_linear_q8(int M, int N, int K, int mode) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 128) throw Error("bad GEMM shape (K must be a multiple of 128)");
+    if (mode != LTX_MODE_F16 && mode != LTX_MODE_BF16 && mode != LTX_MODE_F32) throw Error("unknown mode");
+}
+
 void linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* scales, int scale_f16, const float* bias,
                void* y, int out_f32, int M, int N, int K, int gelu, int mode, const LinearScratch& sc,
                hipStream_t st) {
-    if (M <= 0 || N <= 0 || K <= 0 || K % 128) throw Error("bad GEMM shape (K must be a multiple of 128)");
-    if (mode != LTX_MODE_F16 && mode != LTX_MODE_BF16 && mode != LTX_MODE_F32) throw Error("unknown mode");
+    check_linear_q8(M, N, K, mode);
     if (!a || !q || !scales || !y) throw Error("NULL tensor argument");
     // Borrow the caller's buffers through a non-owning projection view.
     LtxProj p;
@@ -622,6 +635,14 @@ int ltx_block_graph_create(ltx_ctx* c, const ltx_block_weights* w, const float* 
         try {
             ltx::block_forward(c, w, x, tstab, K, tidx, ctx_tokens, S, pts2, cos, sin, T, y, mode, cs);
         } catch (...) {
+            // A throw after the forward forked the context's second stream
+            // into the capture leaves that stream capturing: join it back
+            // into cs, or the capture cannot end and every later forward
+            // would find the second stream still in capture mode.
+            hipStreamCaptureStatus sst = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(c->side, &sst) == hipSuccess && sst == hipStreamCaptureStatusActive &&
+                hipEventRecord(c->side_ev[1], c->side) == hipSuccess)
+                (void)hipStreamWaitEvent(cs, c->side_ev[1], 0);
             (void)hipStreamEndCapture(cs, &graph);
             if (graph) (void)hipGraphDestroy(graph);
             (void)hipStreamDestroy(cs);
@@ -679,6 +700,7 @@ int ltx_op_linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* sca
                      void* y, int out_f32, int M, int N, int K, int gelu, int mode, void* stream) {
     LTX_GUARD(c, {
         if (!c) throw ltx::Error("NULL context");
+        ltx::check_linear_q8(M, N, K, mode);  // before N and K size the scratch
         HIPC(hipSetDevice(c->device));
         ltx::LinearScratch sc{};
         if (ltx::linear_q8_needs_scratch(c, N, K, mode)) {

@@ -21,6 +21,11 @@ struct Error : std::runtime_error {
 
 // Checked HIP call, with the LTX_FAIL_AFTER fault-injection counter.
 void hip_check(hipError_t e, const char* what);
+// LTX_FAIL_CAPTURE=1 (fault injection, like LTX_FAIL_AFTER; read at every
+// call): a block forward being captured into a graph throws right after it
+// forks its second stream into the capture, so that the capture's error path
+// can be tested.
+bool fail_in_capture();
 #define HIPC(x) ::ltx::hip_check((x), #x)
 
 // A device allocation owned by the runtime.
@@ -67,6 +72,10 @@ struct ltx_block_weights {
     ltx::DevBuf qn1, kn1, qn2, kn2;  // f32 [4096]
     ltx::DevBuf sst, psst;    // f32 [9][4096], [2][4096]
     float f16_max = 0.0f;     // largest |weight operand| of mode F16 (above 65504: refused in F16)
+    // async blob uploads: the count of unquantised weights whose f16 copy is
+    // not finite, formed on the device (u64; unallocated for host uploads,
+    // whose f16_max covers them); an F16 forward adds it to the range guard
+    ltx::DevBuf f16_over;
     // f32-mode views of the fused projections' parts (bf16 originals / q8)
     uint64_t bytes = 0;
 };
@@ -147,6 +156,9 @@ struct LinearScratch {
     uint32_t* q;
     uint32_t* pairs;
 };
+// Shape and mode checks of the isolated int8 GEMM (throws Error), made before
+// any scratch is sized from N and K.
+void check_linear_q8(int M, int N, int K, int mode);
 bool linear_q8_needs_scratch(const ltx_ctx* c, int N, int K, int mode);
 void linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* scales, int scale_f16, const float* bias,
                void* y, int out_f32, int M, int N, int K, int gelu, int mode, const LinearScratch& sc,

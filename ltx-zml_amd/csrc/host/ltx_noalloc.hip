@@ -51,7 +51,7 @@ extern "C" int ltx_op_linear_q8_noalloc(ltx_ctx* c, const void* a, const int8_t*
                                         int mode, void* stream) {
     LTX_GUARD(c, {
         if (!c) throw ltx::Error("NULL context");
-        if (M <= 0 || N <= 0 || K <= 0 || K % 128) throw ltx::Error("bad GEMM shape (K must be a multiple of 128)");
+        ltx::check_linear_q8(M, N, K, mode);
         ltx::LinearScratch sc{};
         if (ltx::linear_q8_needs_scratch(c, N, K, mode)) {
             // weights as bytes q + 128, then the scale words, 256-byte aligned

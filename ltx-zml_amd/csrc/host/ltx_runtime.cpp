@@ -23,6 +23,11 @@ static long g_fail_after = [] {
 
 void set_thread_error(const std::string& e) { g_thread_err = e; }
 
+bool fail_in_capture() {  // read at every call (once per forward), so a process can switch it
+    const char* e = std::getenv("LTX_FAIL_CAPTURE");
+    return e && std::atoi(e) != 0;
+}
+
 void hip_check(hipError_t e, const char* what) {
     long n = ++g_hip_calls;
     if (g_fail_after > 0 && n >= g_fail_after && e == hipSuccess) e = hipErrorUnknown;  // injected

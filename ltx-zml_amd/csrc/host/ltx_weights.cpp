@@ -181,7 +181,8 @@ static void check_f32_scales(const void* s, size_t n, const char* what) {
 // |s| for each int8 projection (|q s| <= 128 |s|), max |w| for each bf16
 // weight converted to f16 (projections without int8 companions, gate logits).
 // Above 65504 those operands would round to inf.
-static float f16_operand_max(const void* const* base, const int8_t* const* q8, const void* const* q8s, int sf16) {
+static float f16_operand_max(const void* const* base, const int8_t* const* q8, const void* const* q8s, int sf16,
+                             bool unquantised = true) {
     float m = 0.0f;
     auto bf16_max = [&](int wi, size_t n) {
         const uint16_t* w = (const uint16_t*)base[wi];
@@ -208,7 +209,7 @@ static float f16_operand_max(const void* const* base, const int8_t* const* q8, c
                 smax = std::isnan(v) ? INFINITY : std::max(smax, v);
             }
             m = std::max(m, 128.0f * smax);
-        } else {
+        } else if (unquantised) {
             bf16_max(kQBase[qi], (size_t)O * I);
         }
     }
@@ -398,6 +399,7 @@ struct DevCarve {
     hipStream_t st;
     const char* img;  // device copy of the blob
     bool reuse;
+    unsigned long long* over;  // counts f16 copies that are not finite (the weights' f16_over)
 
     void ensure(DevBuf& d, size_t n) {
         if (reuse) {
@@ -414,7 +416,7 @@ struct DevCarve {
         c->launch("ltx_q8_flip", (unsigned)((n / 4 + 255) / 256), 1, 1, 256, &a, st);
     }
     void cvt(const void* src, void* dst, size_t n, int to_f16) {  // bf16 -> f32 (0) or f16 (1)
-        LtxCvtArgs a{(const uint16_t*)src, dst, n, to_f16};
+        LtxCvtArgs a{(const uint16_t*)src, dst, n, to_f16, to_f16 ? over : nullptr};
         c->launch("ltx_cvt_bf16", (unsigned)((n + 255) / 256), 1, 1, 256, &a, st);
     }
 
@@ -503,7 +505,10 @@ ltx_block_weights* upload_blob_async(ltx_ctx* c, const void* mem, uint64_t mem_b
     // the one DMA of the whole image (asynchronous when `mem` is pinned)
     HIPC(hipMemcpyAsync(c->blob_stage.p, mem, mem_bytes, hipMemcpyHostToDevice, st));
     float f16max;
-    {  // the weight operands' range, read from the host image before the copy
+    {  // the range of the int8 products (scales) and gate weights, read from
+       // the host image; the unquantised projections' f16 copies are counted
+       // on the device as they are made (f16_over), with no host pass over
+       // their ~0.5 GB
         const char* bytes = (const char*)mem;
         const void* base[LTX_W_COUNT];
         for (int i = 0; i < LTX_W_COUNT; i++) base[i] = bytes + L.base[i];
@@ -514,12 +519,14 @@ ltx_block_weights* upload_blob_async(ltx_ctx* c, const void* mem, uint64_t mem_b
                 q8[qi] = (const int8_t*)(bytes + L.q8[qi]);
                 q8s[qi] = bytes + L.q8s[qi];
             }
-        f16max = f16_operand_max(base, q8, q8s, L.sf16);
+        f16max = f16_operand_max(base, q8, q8s, L.sf16, false);
     }
     ltx_block_weights* w = reuse ? reuse : new ltx_block_weights();
     w->f16_max = f16max;
     try {
-        DevCarve d{c, st, (const char*)c->blob_stage.p, reuse != nullptr};
+        if (!w->f16_over.p) w->f16_over.alloc(sizeof(unsigned long long));
+        HIPC(hipMemsetAsync(w->f16_over.p, 0, sizeof(unsigned long long), st));
+        DevCarve d{c, st, (const char*)c->blob_stage.p, reuse != nullptr, (unsigned long long*)w->f16_over.p};
         d.proj(w->qkv1, L, {LTX_Q_Q1, LTX_Q_K1, LTX_Q_V1}, LTX_D, true);
         d.proj(w->o1, L, {LTX_Q_O1}, LTX_D, true);
         d.proj(w->q2, L, {LTX_Q_Q2}, LTX_D, true);

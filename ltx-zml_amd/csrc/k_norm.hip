@@ -39,6 +39,7 @@ __device__ void norm_mod_body(const LtxNormArgs& a) {
     };
     if (shared_mod) load_mod(ada_row(a.ada, row0));
     unsigned bad = 0;  // 16-bit stores out of range (range guard)
+    if (a.sat_add && blockIdx.x == 0 && threadIdx.x == 0 && a.sat) atomicAdd(a.sat, *a.sat_add);
     for (int k = 0; k < nr; k++) {
         const int row = row0 + k;
         const float4* x = (const float4*)(a.x + (size_t)row * LTX_D);
@@ -349,10 +350,13 @@ extern "C" __global__ void __launch_bounds__(256) ltx_cvt_bf16(const LtxCvtArgs 
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= a.n) return;
     const float v = __builtin_bit_cast(float, (uint32_t)a.in[i] << 16);
-    if (a.to_f16)
-        ((_Float16*)a.out)[i] = (_Float16)v;
-    else
+    if (a.to_f16) {
+        const _Float16 h = (_Float16)v;
+        ((_Float16*)a.out)[i] = h;
+        range_report(a.over, __builtin_isfinite((float)h) ? 0u : 1u);
+    } else {
         ((float*)a.out)[i] = v;
+    }
 }
 
 extern "C" __global__ void __launch_bounds__(256) ltx_q8_flip(const LtxFlipArgs a) {

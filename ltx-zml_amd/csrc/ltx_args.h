@@ -38,6 +38,7 @@ typedef struct {
     int rows;
     int ish, isc;    // ada row indices for shift and scale; isc < 0: plain rms
     unsigned long long* sat;  // range guard counter (16-bit outputs) or NULL
+    const unsigned long long* sat_add;  // or NULL: a count the first workgroup adds to sat
 } LtxNormArgs;
 
 // Cross-attention K/V modulation (ltx/block.zig:553-556):
@@ -160,12 +161,14 @@ typedef struct {
 } LtxDequantArgs;
 
 // bf16 -> f32 (to_f16 = 0) or f16 (to_f16 = 1, round to nearest even), n
-// elements.
+// elements. over (f16 only, or NULL): counts the values whose f16 is not
+// finite (beyond 65504, or not finite already).
 typedef struct {
     const uint16_t* in;
     void* out;
     size_t n;
     int to_f16;
+    unsigned long long* over;
 } LtxCvtArgs;
 
 // int8 weights -> bytes q + 128 (XOR 0x80 per byte), n words of 4 bytes.

@@ -29,8 +29,11 @@ def _eager(ctx, w, d, cos, sin, y, mode):
     ctx.forward(w, d["x"], d["tstab"], d["tidx"], d["ctx"], d["pts2"], cos, sin, y, mode=mode)
 
 
-@pytest.mark.parametrize("mode,T,S", [("f16", 256, 64), ("f16", 250, 40), ("bf16", 256, 64), ("f32", 128, 32)])
+@pytest.mark.parametrize("mode,T,S", [("f16", 256, 64), ("f16", 250, 40), ("bf16", 256, 64), ("f32", 128, 32),
+                                      ("f16", 8192, 256)])
 def test_block_graph_matches_eager(ctx, block0, mode, T, S):
+    """T = 8,192 takes the large-T kernel choices and records the marker
+    events after the launches around the second stream (from 8,192 tokens)."""
     say(f"block graph mode={mode} T={T} S={S}")
     md = rt.MODES[mode]
     w = ctx.upload(block0)
@@ -106,3 +109,36 @@ def test_block_graph_refused_while_profiling(ctx, block0):
     finally:
         ctx.profile(False)
     w.free()
+
+
+def test_graph_capture_failure_leaves_context_usable(ctx, block0, monkeypatch):
+    """A forward that throws inside the capture, after its second stream
+    joined it (LTX_FAIL_CAPTURE), fails ltx_block_graph_create with that
+    error; the capture is ended with the second stream joined back, so the
+    context's eager forwards and a later graph still match the forward from
+    before, bit for bit."""
+    T, S = 256, 64
+    say(f"graph capture failure T={T} S={S}")
+    md = rt.MODES["f16"]
+    w = ctx.upload(block0)
+    d, cos, sin = _inputs(T, S)
+    want = torch.empty((T, 4096), dtype=torch.float32, device="cuda")
+    _eager(ctx, w, d, cos, sin, want, md)
+    torch.cuda.synchronize()
+    y = torch.empty_like(want)
+    monkeypatch.setenv("LTX_FAIL_CAPTURE", "1")
+    with pytest.raises(rt.LtxError, match="LTX_FAIL_CAPTURE"):
+        ctx.block_graph(w, d["x"], d["tstab"], d["tidx"], d["ctx"], d["pts2"], cos, sin, y, mode=md)
+    monkeypatch.delenv("LTX_FAIL_CAPTURE")
+    _eager(ctx, w, d, cos, sin, y, md)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), want.view(torch.int32))
+    y.fill_(float("nan"))
+    g = ctx.block_graph(w, d["x"], d["tstab"], d["tidx"], d["ctx"], d["pts2"], cos, sin, y, mode=md)
+    try:
+        g.launch()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), want.view(torch.int32))
+    finally:
+        g.free()
+        w.free()

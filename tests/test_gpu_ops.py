@@ -464,3 +464,25 @@ def test_upload_refuses_f32_scales_out_of_range(ctx, block0):
         q8s["k1"] = s
         with pytest.raises(rt.LtxError, match="ScaleRange"):
             ctx.upload(bf.BlockTensors(0, block0.base, block0.q8, q8s))
+
+
+@pytest.mark.parametrize("noalloc", [False, True])
+def test_linear_q8_rejects_bad_arguments_before_allocating(ctx, noalloc):
+    """Invalid shapes and modes are refused by name before N and K size any
+    scratch (a negative N once reached the allocation as a wrapped size).
+    Nothing is launched: every call fails its checks first."""
+    say(f"linear_q8 argument checks noalloc={noalloc}")
+    a = torch.zeros((4, 128), dtype=torch.float16, device="cuda")
+    q = torch.zeros((256, 128), dtype=torch.int8, device="cuda")
+    s = torch.ones((256, 1), dtype=torch.float16, device="cuda")
+    y = torch.empty((4, 256), dtype=torch.float16, device="cuda")
+    name = "ltx_op_linear_q8_noalloc" if noalloc else "ltx_op_linear_q8"
+    fn = getattr(rt.lib(), name)
+    st = torch.cuda.current_stream().cuda_stream
+    cases = [(4, -256, 128, rt.MODE_F16, "bad GEMM shape"), (4, 256, 0, rt.MODE_F16, "bad GEMM shape"),
+             (4, 256, 100, rt.MODE_F16, "bad GEMM shape"), (0, 256, 128, rt.MODE_F16, "bad GEMM shape"),
+             (4, 256, 128, 7, "unknown mode")]
+    for M, N, K, mode, msg in cases:
+        with pytest.raises(rt.LtxError, match=msg):
+            ctx._check(fn(ctx.handle, a.data_ptr(), q.data_ptr(), s.data_ptr(), 1, None, y.data_ptr(), 0, M, N, K, 0,
+                          mode, st), name)

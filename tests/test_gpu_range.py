@@ -3,7 +3,9 @@
 The reference computes in f32; the fp16 mode stores the MFMA operands in
 f16, whose largest finite value is 65504. The block counts, on the device,
 every 16-bit store that is not finite or beyond that, and a forward in fp16
-mode refuses weights whose f16 operands would exceed it. Checked here:
+mode refuses weights whose f16 operands would exceed it (the streaming
+upload counts its unquantised weights' f16 copies on the device instead).
+Checked here:
 - AdaLN rows of order 1 (instead of the synthetic tables' 0.1) and
   Student-t(3) activations: nothing out of range, and the block still within
   the fp16 gate of the f64 oracle;
@@ -105,3 +107,36 @@ def test_f16_mode_refuses_weights_beyond_f16(ctx, block0_out):
     torch.cuda.synchronize()
     w.free()
     assert torch.isfinite(y).all().item()
+
+
+def test_async_upload_counts_unquantised_weights_beyond_f16(ctx, block0_w16):
+    """The streaming upload makes the f16 copies of unquantised weights on the
+    device and counts those that are not finite there (no host pass over
+    them); a forward in fp16 mode adds that count to the range guard, one in
+    bf16 mode does not. One bf16 weight of 1e5 in ff1: at least that one
+    count in fp16 mode; none for the same weights in bf16 mode, and none for
+    the unmodified block in fp16 mode."""
+    say("range guard: async-uploaded bf16 weight 1e5 -> counted in f16, not in bf16")
+    base = dict(block0_w16.base)
+    w1 = base["ff1_w"].copy()
+    w1[5, 7] = bf.bf16_bits(np.array([1.0e5], np.float32))[0]
+    base["ff1_w"] = w1
+    big = bf.BlockTensors(0, base, {}, {})
+    inp = synth.make_inputs(T, S, sigma=0.7)
+    cos, sin = rt.rope_tables(inp["grid"])
+    counts = {}
+    for name, bt in (("big", big), ("plain", block0_w16)):
+        blob, man = bf.pack(bt)
+        pin = torch.empty(len(blob), dtype=torch.uint8).pin_memory()
+        pin.numpy()[:] = np.frombuffer(blob, dtype=np.uint8)
+        st = torch.cuda.Stream()
+        w = ctx.upload_blob_async(pin.data_ptr(), len(blob), bf.manifest_json(man), bt.block, stream=st)
+        st.synchronize()
+        for mode in ("f16", "bf16"):
+            ctx.range_count(reset=True)
+            forward(ctx, w, inp, cos, sin, mode)
+            counts[(name, mode)] = ctx.range_count(reset=True)
+        w.free()
+    say(f"  counts {counts}")
+    assert counts[("big", "f16")] >= 1
+    assert counts[("big", "bf16")] == 0 and counts[("plain", "f16")] == 0
