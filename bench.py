@@ -33,7 +33,7 @@ PEAK_F32_TFLOPS = 157.3  # MI355X fp32 (the f32 mode's kernels are SIMT f32)
 # FETCH_SIZE x 2.0 (the factor a 1 GiB copy calibrates) + WRITE_SIZE x 1.0,
 # measured on this kernel (profiles/block_t28672_hbm_bytes.md); None for a
 # size or type not profiled.
-ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.473e9, (28672, "bf16"): 2.470e9}
+ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.475e9, (28672, "bf16"): 2.470e9}
 
 
 def flops(T: int, S: int) -> dict:
@@ -167,9 +167,9 @@ def cpu_baseline(T: int, S: int, threads: int, small=None, full=None) -> dict:
             t5 = time.perf_counter()
             oracle.block_forward(bt0, inp0, c0, s0, chunk=1024, real="f32")
             runs.append(time.perf_counter() - t5)
-        extra = {"t1024_block_ms_p50": round(1e3 * sorted(runs)[2], 1),
-                 "t1024_sample": "the whole f32 block at T = 1,024, S = 128 (N(0, 0.02) weights, fp16 scales, "
-                                 "sigma 0.5): one warm-up, median of 5"}
+        extra.update({"t1024_block_ms_p50": round(1e3 * sorted(runs)[2], 1),
+                      "t1024_sample": "the whole f32 block at T = 1,024, S = 128 (N(0, 0.02) weights, fp16 scales, "
+                                      "sigma 0.5): one warm-up, median of 5"})
     head = (f"f32 CPU restatement of the reference graph (ZML CPU-PJRT unavailable offline), OpenMP "
             f"{threads} threads: ")
     rates = (f"int8-dequant GEMM at the ff1 shape on {m1} and {m2} rows ({rate / 1e9:.1f} GFLOP/s marginal), "
@@ -376,6 +376,29 @@ def sweep_bench(args) -> int:
                          "tflops": round(tf, 1), "frac": round(tf / PEAK_TFLOPS, 4)})
             del a, y
         del dq, scales
+        if args.dense:
+            # comparison only: torch's 16-bit matmul (hipBLASLt on ROCm) on the
+            # same shape with the weight as a Linear layer holds it ([N][K],
+            # the "NT" layout) and twice the weight bytes, no dequantisation
+            for mode in modes:
+                dt = torch.float16 if mode == "f16" else torch.bfloat16
+                a = torch.randn((M, K), dtype=dt, device="cuda")
+                wd = (torch.randn((N, K), dtype=torch.float32, device="cuda") * 0.02).to(dt)
+                st = torch.cuda.current_stream()
+                for _ in range(max(args.warmup, 1)):
+                    y = a @ wd.t()
+                ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+                ev[0].record(st)
+                for _ in range(reps):
+                    y = a @ wd.t()
+                ev[1].record(st)
+                torch.cuda.synchronize()
+                ms = ev[0].elapsed_time(ev[1]) / reps
+                tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+                log(f"bench: dense {M}x{K}x{N} {mode} (hipBLASLt, 16-bit weights): {ms:.3f} ms, {tf:.0f} TFLOP/s")
+                rows.append({"kernel": "dense_matmul", "M": M, "K": K, "N": N, "dtype": mode, "ms": round(ms, 4),
+                             "tflops": round(tf, 1), "frac": round(tf / PEAK_TFLOPS, 4)})
+                del a, wd, y
         torch.cuda.empty_cache()
     for lq, lkv in ATTN_SWEEP:
         for mode in modes:
@@ -422,6 +445,8 @@ def main() -> int:
     ap.add_argument("--scales", default="f16", choices=["f16", "f32"],
                     help="scale type of the int8 weights: fp16 (the benchmark configuration) or f32 (the "
                          "reference packer's version-1 format)")
+    ap.add_argument("--dense", action="store_true",
+                    help="with --sweep: also time torch's 16-bit matmul (hipBLASLt) at the GEMM shapes, as a comparison")
     ap.add_argument("--sweep", action="store_true",
                     help="instead of the block line: time the isolated GEMM and attention kernels at the "
                          "microbenchmark shapes (f16 and bf16 operands) and print their own JSON line")

@@ -188,7 +188,11 @@ int ltx_block_stage(ltx_ctx* ctx, int stage, void** dev_ptr, uint64_t* bytes);
  * 0). A non-zero count means some activation left the 16-bit range: rerun in
  * LTX_MODE_BF16 (the f32 exponent range) or LTX_MODE_F32. Weight operands
  * are checked at upload instead: a forward in LTX_MODE_F16 refuses a block
- * whose dequantised weights (128 |s|) or f16 copies exceed 65504. */
+ * whose dequantised weights (128 |s|) or f16 copies exceed 65504. Weights
+ * from ltx_block_weights_from_blob_async are checked the same way except the
+ * f16 copies of unquantised projections, which are made on the device: the
+ * copies that are not finite are counted there, and every LTX_MODE_F16
+ * forward with those weights adds that count to this counter. */
 int ltx_range_count(ltx_ctx* ctx, void* stream, uint64_t* count, int reset);
 
 /* ---- isolated operators (the microbenchmark surface, ltx/smoke.zig) ---- */
@@ -202,7 +206,9 @@ int ltx_range_count(ltx_ctx* ctx, void* stream, uint64_t* count, int reset);
  * [K/128][N] in scratch the context owns (allocated on first use, grown as
  * needed) and then runs the GEMM, all on `stream`: two calls of one context on
  * different streams may overwrite each other's scratch, so keep one context's
- * calls on one stream. */
+ * calls on one stream. A shape with M, N or K not positive or K not a
+ * multiple of 128, or an unknown mode, is refused (status 0, ltx_last_error)
+ * before any scratch is sized or allocated. */
 int ltx_op_linear_q8(ltx_ctx* ctx, const void* a, const int8_t* q, const void* scales, int scale_f16,
                      const float* bias, void* y, int out_f32, int M, int N, int K, int gelu, int mode,
                      void* stream);
