@@ -318,7 +318,7 @@ def denoise_bench(args) -> int:
 # launch labels of one block forward (a label covers every launch whose name
 # contains it): ms per launch at T = 28,672, ms per forward at T = 1,024
 KERNEL_LABELS = ("attn:self", "attn:cross", "gemm:qkv1", "gemm:o1", "gemm:q2", "gemm:kv2", "gemm:o2", "gemm:ff1",
-                 "gemm:ff2", "ltx_norm_mod", "ltx_qknorm", "ltx_gate", "ltx_enc", "splitk_reduce")
+                 "gemm:ff2", "dq16", "ltx_norm_mod", "ltx_qknorm", "ltx_gate", "ltx_enc", "splitk_reduce")
 
 GEMM_SWEEP = [(4096, 4096, 4096), (28672, 4096, 4096), (28672, 4096, 16384), (28672, 16384, 4096)]  # M, K, N
 ATTN_SWEEP = [(4096, 4096), (16384, 16384), (28672, 28672), (28672, 256)]  # Lq, Lkv
@@ -344,7 +344,9 @@ def sweep_bench(args) -> int:
     reps = max(args.steps, 1)
     rows = []
 
-    def timed(fn, substr):
+    def timed(fn, substr, *more):
+        """Kernel time per call of fn, summed over the launches whose names
+        contain substr (and, as further values, each of `more`)."""
         for _ in range(max(args.warmup, 1)):
             fn()
         torch.cuda.synchronize()
@@ -352,9 +354,9 @@ def sweep_bench(args) -> int:
         ctx.profile_reset()
         for _ in range(reps):
             fn()
-        tot, n = ctx.profile_read(substr)
+        out = [ctx.profile_read(x)[0] / reps for x in (substr,) + more]
         ctx.profile(False)
-        return tot / max(n, 1)
+        return out[0] if not more else out
 
     for M, K, N in GEMM_SWEEP:
         g = np.random.default_rng(M + 3 * K + 7 * N)
@@ -368,12 +370,14 @@ def sweep_bench(args) -> int:
             ds = scales[sdt]
             a = torch.randn((M, K), dtype=dt, device="cuda")
             y = torch.empty((M, N), dtype=dt, device="cuda")
-            ms = timed(lambda: ctx.linear_q8(a, dq, ds, None, y, mode=rt.MODES[mode]), "ltx_gemm")
+            ms, ms_dq = timed(lambda: ctx.linear_q8(a, dq, ds, None, y, mode=rt.MODES[mode]), "ltx_gemm",
+                              "ltx_gemm_dq16")
             assert torch.isfinite(y).all().item(), "non-finite GEMM output"
             tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-            log(f"bench: gemm {M}x{K}x{N} {mode} {sdt} scales: {ms:.3f} ms, {tf:.0f} TFLOP/s")
+            log(f"bench: gemm {M}x{K}x{N} {mode} {sdt} scales: {ms:.3f} ms (dequantisation {ms_dq:.3f}), "
+                f"{tf:.0f} TFLOP/s")
             rows.append({"kernel": "gemm", "M": M, "K": K, "N": N, "dtype": mode, "scales": sdt, "ms": round(ms, 4),
-                         "tflops": round(tf, 1), "frac": round(tf / PEAK_TFLOPS, 4)})
+                         "dequant_ms": round(ms_dq, 4), "tflops": round(tf, 1), "frac": round(tf / PEAK_TFLOPS, 4)})
             del a, y
         del dq, scales
         if args.dense:
@@ -551,7 +555,9 @@ def main() -> int:
     peak = PEAK_F32_TFLOPS if args.mode == "f32" else PEAK_TFLOPS
     attn_ms = per["attn:self"]
     achieved = f["self_attn"] / (attn_ms * 1e-3) / 1e12
-    gemm_ms = sum(v for k, v in per.items() if k.startswith("gemm:"))
+    # the GEMMs' time includes the dequantisation of the int8 weights that the
+    # four-wave GEMM takes (label dq16)
+    gemm_ms = sum(v for k, v in per.items() if k.startswith("gemm:")) + per["dq16"]
     log(f"bench: block {ms:.2f} ms (as a graph {ms_graph:.2f} ms), self-attn {attn_ms:.2f} ms, GEMMs {gemm_ms:.2f} ms")
     res = {
         "metric": "int8 DiT-block ms + % bf16 MFMA peak @28,672 tok; attention TFLOP/s",

@@ -88,9 +88,14 @@ __device__ __forceinline__ void gemm_epilogue(const LtxGemmArgs& a, const f32x16
 // move with non-temporal loads and stores: each is touched once here, and
 // kept out of the way of the A and W tiles in L2 they took o1 and o2 1.2-1.6 %
 // faster and the RMSNorm + modulate that reads x_sa 1.6 % faster.
-template <typename T, int EPI, int NI, int NJ>
-__device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f32x16 (&acc)[NI][NJ], float* patch,
-                                                  int mw, int nw, int n0) {
+//
+// The patch is filled by fill(i, patch, LD) with the wave's accumulators of
+// 32-row block i (row r of the block at patch[r * LD + column]), so kernels
+// with other MFMA layouts share everything after it; gemm_epilogue_lds below
+// is the form for NI x NJ blocks of 32 x 32.
+template <typename T, int EPI, int NI, int NJ, typename Fill>
+__device__ __forceinline__ void gemm_epilogue_patch(const LtxGemmArgs& a, Fill fill, float* patch, int mw, int nw,
+                                                    int n0) {
     constexpr int WN = 32 * NJ, LD = WN + 8;
     const int lane = threadIdx.x & 63;
     const bool vt = EPI == LTX_EPI_QKV && n0 >= a.nsplit;
@@ -127,11 +132,7 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
 #pragma unroll
                 for (int p = 0; p < RNP; p++) tixn[p] = ada_row(a.ada, min(mb + 32 + r0 + RRPP * p, a.M - 1));
         }
-#pragma unroll
-        for (int j = 0; j < NJ; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++)
-                patch[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * LD + 32 * j + (lane & 31)] = acc[i][j][r];
+        fill(i, patch, LD);
         if (vt) {
             // V^T [c][m]: 4 lanes cover one column's 32 rows (64 contiguous bytes)
             const int rg = lane & 3;
@@ -205,6 +206,22 @@ __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f3
         }
     }
     range_report(a.sat, bad);
+}
+
+template <typename T, int EPI, int NI, int NJ>
+__device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f32x16 (&acc)[NI][NJ], float* patch,
+                                                  int mw, int nw, int n0) {
+    const int lane = threadIdx.x & 63;
+    gemm_epilogue_patch<T, EPI, NI, NJ>(
+        a,
+        [&](int i, float* p, int LD) {
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    p[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * LD + 32 * j + (lane & 31)] = acc[i][j][r];
+        },
+        patch, mw, nw, n0);
 }
 
 // Split-K partial sums: one wave's (32 NI) x (32 NJ) f32 accumulators to

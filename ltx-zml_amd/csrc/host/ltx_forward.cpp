@@ -30,7 +30,13 @@ struct Carve {
 struct Ws16 {
     void *n_msa, *qk16, *vt1, *qh1, *kh1, *glog1, *o1, *x_sa, *attn_in, *q2_16, *glog2, *enc, *k2_16, *vt2, *qh2,
         *kh2, *o2, *x_ca, *ff_in, *h, *part;
+    void* dq[6];  // 16-bit weights of qkv1, o1, q2, o2, ff1, ff2 for the four-wave GEMM (NULL: not used)
 };
+
+// The projections the four-wave GEMM may take, as (N, K) with A rows of K
+// elements and M = T: qkv1, o1, q2, o2, ff1, ff2.
+static const int kX4Shapes[6][2] = {{3 * LTX_D, LTX_D}, {LTX_D, LTX_D}, {LTX_D, LTX_D},
+                                    {LTX_D, LTX_D},     {LTX_FF, LTX_D}, {LTX_D, LTX_FF}};
 
 // Split-K slices of a GEMM whose 256 x tn output tiles would fill at most
 // half the CUs: the largest power of two S <= 8 with tiles * S <= CUs and
@@ -42,8 +48,19 @@ static int gemm_ksplit(int num_cu, int M, int N, int K, int tn = 256) {
     return s;
 }
 
-static void carve16(Carve& c, Ws16& w, size_t T, size_t S, int num_cu) {
+bool x4_shape(const ltx_ctx* c, int mode, int M, int N, int K, int lda) {
+    if (mode != LTX_MODE_F16 && mode != LTX_MODE_BF16) return false;
+    if (!c->gemm_x4 || !c->gemm_dma) return false;
+    if (M <= 0 || N % 256 || K % 128 || lda < K || lda % 8) return false;
+    if ((uint64_t)M * lda * 2 >= (1ull << 31) || (uint64_t)N * K * 2 >= (1ull << 31)) return false;
+    if (c->gemm_x4 == 2) return true;
+    // where its 256 x 256 tiles fill the CUs: the sizes that need no split-K
+    return M >= 4096 && gemm_ksplit(c->num_cu, M, N, K) == 1;
+}
+
+static void carve16(Carve& c, Ws16& w, size_t T, size_t S, const ltx_ctx* ctx, int mode) {
     const size_t D = LTX_D;
+    const int num_cu = ctx->num_cu;
     w.n_msa = c.take(T * D * 2);
     w.qk16 = c.take(T * 2 * D * 2);
     w.vt1 = c.take(T * D * 2);
@@ -74,6 +91,10 @@ static void carve16(Carve& c, Ws16& w, size_t T, size_t S, int num_cu) {
         if (k > 1) part = std::max(part, (size_t)k * sh[0] * sh[1] * 4);
     }
     w.part = part ? c.take(part) : nullptr;
+    for (int i = 0; i < 6; i++) {
+        const int N = kX4Shapes[i][0], K = kX4Shapes[i][1];
+        w.dq[i] = x4_shape(ctx, mode, (int)T, N, K, K) ? c.take((size_t)N * K * 2) : nullptr;
+    }
 }
 
 struct Ws32 {
@@ -108,7 +129,7 @@ static void ensure_ws(ltx_ctx* c, size_t T, size_t S, int mode) {
         carve32(cv, w, T, S);
     } else {
         Ws16 w;
-        carve16(cv, w, T, S, c->num_cu);
+        carve16(cv, w, T, S, c, mode);
     }
     if (c->ws.bytes < cv.off) {
         if (c->ws_pins)
@@ -144,9 +165,11 @@ static void norm_mod(ltx_ctx* c, int mode, const float* x, void* y, LtxAda ada, 
     c->launch(k, (rows + 3) / 4, 1, 1, 256, &a, st);  // four rows per workgroup (NORM_ROWS)
 }
 
-// 16-bit GEMM: y = A . W^T with the given epilogue.
+// 16-bit GEMM: y = A . W^T with the given epilogue. w16: the int8
+// projection's weights dequantised to the operand type for this call (by
+// dequant16), which routes it to the four-wave kernel, or NULL.
 static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M, int lda, int epi, LtxGemmArgs g,
-                   hipStream_t st, const char* label = nullptr) {
+                   hipStream_t st, const char* label = nullptr, const void* w16 = nullptr) {
     if (p.N % 256 != 0 || p.K % 64 != 0) throw Error("gemm16: N must be a multiple of 256 and K of 64");
     g.a = A;
     g.M = M;
@@ -169,15 +192,31 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
     g.tiles_m = (M + 255) / 256;
     g.tiles_n = p.N / 256;
     char name[64];
+    auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+    const char* es = epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv";
+    // Four-wave 16-bit kernel: unquantised weights, or int8 weights
+    // dequantised for this call; 16-byte aligned operands (its DMA and
+    // epilogue move 16-byte vectors)
+    {
+        const void* wb = p.q8 ? w16 : (mode == LTX_MODE_BF16 ? p.w_bf16.p : p.w_f16.p);
+        if (wb && x4_shape(c, mode, M, p.N, p.K, lda) && g.ldo % 8 == 0 && al16(A) && al16(wb) && al16(g.out) &&
+            al16(g.out2) && al16(g.resid) && al16(g.bias) && al16(g.ada.tstab) && al16(g.ada.sst)) {
+            g.b = wb;
+            g.scales = nullptr;
+            g.ksplit = 1;
+            std::snprintf(name, sizeof(name), "ltx_gemm_x4_%s_%s", msuffix(mode), es);
+            const int nitems = g.tiles_m * g.tiles_n;
+            c->launch(name, c->gemm_persistent ? std::min(nitems, c->num_cu) : nitems, 1, 1, 256, &g, st, label);
+            return;
+        }
+    }
     // LDS-DMA int8 kernel: f16 or bf16 operands, f16 scales, K a multiple of
     // 128, and byte offsets of A and W within 31 bits (32-bit buffer offsets)
-    auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
     if ((mode == LTX_MODE_F16 || mode == LTX_MODE_BF16) && p.q8 && p.qflip && p.s2.p &&
         c->gemm_dma && p.K % 128 == 0 && (uint64_t)M * lda * 2 < (1ull << 31) && (uint64_t)p.N * p.K < (1ull << 31) && g.ldo % 8 == 0 &&
         al16(g.out) && al16(g.out2) && al16(g.resid) && al16(g.bias) && al16(g.ada.tstab) && al16(g.ada.sst)) {
         // (its epilogue moves 16-byte vectors: outputs, residual and bias 16-byte aligned)
         g.scales = p.s2.p;
-        const char* es = epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv";
         std::snprintf(name, sizeof(name), "ltx_gemm_q8_%s%s%s", mode == LTX_MODE_BF16 ? "bf16_" : "",
                       p.scale_f16 ? "" : "s32_", es);
         // few output tiles: split K over more workgroups (when the caller
@@ -191,7 +230,6 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
         }
         return;
     }
-    const char* es = epi == LTX_EPI_STORE ? "store" : epi == LTX_EPI_RESID_GATE ? "resid" : "qkv";
     // LDS-DMA 16-bit-weight kernel (256 x 128 tiles): the same conditions
     if ((mode == LTX_MODE_F16 || mode == LTX_MODE_BF16) && !p.q8 && c->gemm_dma && p.K % 128 == 0 &&
         p.N % 128 == 0 && (uint64_t)M * lda * 2 < (1ull << 31) && (uint64_t)p.N * p.K * 2 < (1ull << 31) &&
@@ -218,6 +256,37 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
     if (g.ksplit > 1) {
         std::snprintf(name, sizeof(name), "ltx_gemm_reduce_%s_%s", msuffix(mode), es);
         c->launch(name, p.N / 64, (M + 63) / 64, 1, 256, &g, st, "splitk_reduce");
+    }
+}
+
+// Dequantises the int8 projections p[i] whose buffer out[i] is set (and whose
+// weights are laid out for the LDS-DMA kernels: bytes q + 128, scale words)
+// into out[i], one launch per scale type; done[i] = out[i] for those, NULL
+// for the rest.
+static void dequant16(ltx_ctx* c, int mode, const LtxProj* const* p, void* const* out, int n, const void** done,
+                      hipStream_t st) {
+    for (int sf = 0; sf < 2; sf++) {  // f16 scale pairs, then f32 scales
+        LtxDq16Args a{};
+        int nb = 0;
+        for (int i = 0; i < n; i++) {
+            if (sf == 0) done[i] = nullptr;
+            const LtxProj& q = *p[i];
+            if (!out[i] || !q.q8 || !q.qflip || !q.s2.p || (q.scale_f16 ? 0 : 1) != sf) continue;
+            const int j = a.njobs++;
+            a.q[j] = (const uint8_t*)q.q.p;
+            a.s2[j] = (const uint32_t*)q.s2.p;
+            a.out[j] = out[i];
+            a.N[j] = q.N;
+            a.K[j] = q.K;
+            a.start[j] = nb;
+            nb += (q.K / LTX_GROUP) * ((q.N + 31) / 32);
+            done[i] = out[i];
+        }
+        if (!a.njobs) continue;
+        a.start[a.njobs] = nb;
+        char name[48];
+        std::snprintf(name, sizeof(name), "ltx_gemm_dq16_%s%s", msuffix(mode), sf ? "_s32" : "");
+        c->launch(name, nb, 1, 1, 256, &a, st, "dq16");
     }
 }
 
@@ -410,7 +479,14 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
                     std::to_string(w->f16_max) + " > 65504); run LTX_MODE_BF16");
     unsigned long long* sat = sat_of(c, mode);
     Ws16 b;
-    carve16(cv, b, T, S, c->num_cu);
+    carve16(cv, b, T, S, c, mode);
+    // the int8 weights of the projections on the four-wave GEMM, dequantised
+    // for this forward (qkv1, o1, q2, o2, ff1, ff2)
+    const void* dq[6];
+    {
+        const LtxProj* ps[6] = {&w->qkv1, &w->o1, &w->q2, &w->o2, &w->f1, &w->f2};
+        dequant16(c, mode, ps, b.dq, 6, dq, st);
+    }
     // self-attention: n = modulate(rms(x), ada1, ada0); fused q|k|v GEMM
     norm_mod(c, mode, x, b.n_msa, ada, T, 0, 1, st,
              mode == LTX_MODE_F16 ? (const unsigned long long*)w->f16_over.p : nullptr);
@@ -420,7 +496,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.nsplit = 2 * LTX_D;
     g.sat = sat;
     g.part = (float*)b.part;  // split-K partial sums (small grids)
-    gemm16(c, mode, w->qkv1, b.n_msa, T, LTX_D, LTX_EPI_QKV, g, st, "gemm:qkv1");
+    gemm16(c, mode, w->qkv1, b.n_msa, T, LTX_D, LTX_EPI_QKV, g, st, "gemm:qkv1", dq[0]);
     // The self-attention gate logits on the side stream, beside the q/k
     // norms (both read only what the GEMMs above wrote). Side work starts
     // after the persistent GEMM before it, whose one-workgroup-per-CU grid it
@@ -448,7 +524,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.igate = 2;
     g.ldo = LTX_D;
     g.part = (float*)b.part;  // split-K partial sums (small grids)
-    gemm16(c, mode, w->o1, b.o1, T, LTX_D, LTX_EPI_RESID_GATE, g, st, "gemm:o1");
+    gemm16(c, mode, w->o1, b.o1, T, LTX_D, LTX_EPI_RESID_GATE, g, st, "gemm:o1", dq[1]);
     // cross-attention
     norm_mod(c, mode, (const float*)b.x_sa, b.attn_in, ada, T, 6, 7, st);
     g = LtxGemmArgs{};
@@ -456,7 +532,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.ldo = LTX_D;
     g.sat = sat;
     g.part = (float*)b.part;  // split-K partial sums (small grids)
-    gemm16(c, mode, w->q2, b.attn_in, T, LTX_D, LTX_EPI_STORE, g, st, "gemm:q2");
+    gemm16(c, mode, w->q2, b.attn_in, T, LTX_D, LTX_EPI_STORE, g, st, "gemm:q2", dq[2]);
     {
         // A marker after each launch from here to the cross-attention (see
         // ltx_ctx::launch): without them the gate logits below and the k|v
@@ -488,7 +564,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.igate = 8;
     g.ldo = LTX_D;
     g.part = (float*)b.part;  // split-K partial sums (small grids)
-    gemm16(c, mode, w->o2, b.o2, T, LTX_D, LTX_EPI_RESID_GATE, g, st, "gemm:o2");
+    gemm16(c, mode, w->o2, b.o2, T, LTX_D, LTX_EPI_RESID_GATE, g, st, "gemm:o2", dq[3]);
     // feed-forward
     norm_mod(c, mode, (const float*)b.x_ca, b.ff_in, ada, T, 3, 4, st);
     g = LtxGemmArgs{};
@@ -497,7 +573,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.gelu = 1;
     g.sat = sat;
     g.part = (float*)b.part;  // split-K partial sums (small grids)
-    gemm16(c, mode, w->f1, b.ff_in, T, LTX_D, LTX_EPI_STORE, g, st, "gemm:ff1");
+    gemm16(c, mode, w->f1, b.ff_in, T, LTX_D, LTX_EPI_STORE, g, st, "gemm:ff1", dq[4]);
     g = LtxGemmArgs{};
     g.out = y;
     g.resid = (const float*)b.x_ca;
@@ -505,7 +581,7 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.igate = 5;
     g.ldo = LTX_D;
     g.part = (float*)b.part;  // split-K partial sums (small grids)
-    gemm16(c, mode, w->f2, b.h, T, LTX_FF, LTX_EPI_RESID_GATE, g, st, "gemm:ff2");
+    gemm16(c, mode, w->f2, b.h, T, LTX_FF, LTX_EPI_RESID_GATE, g, st, "gemm:ff2", dq[5]);
 
     set_stage(c, LTX_ST_NORM_MSA, b.n_msa, TD * 2);
     set_stage(c, LTX_ST_Q1, b.qh1, TD * 2);
@@ -572,12 +648,19 @@ void linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* scales, i
                 p.q.p = sc.q;
                 p.qflip = true;
             }
+            // the four-wave kernel on the weights dequantised into sc.w16
+            const void* w16 = nullptr;
+            if (sc.w16 && p.qflip && x4_shape(c, mode, M, N, K, K)) {
+                const LtxProj* ps[1] = {&p};
+                void* outs[1] = {sc.w16};
+                dequant16(c, mode, ps, outs, 1, &w16, st);
+            }
             LtxGemmArgs g{};
             g.out = y;
             g.ldo = N;
             g.gelu = gelu;
             g.out_f32 = out_f32;
-            gemm16(c, mode, p, a, M, K, LTX_EPI_STORE, g, st);
+            gemm16(c, mode, p, a, M, K, LTX_EPI_STORE, g, st, nullptr, w16);
         }
     } catch (...) {
         p.q.p = p.s.p = p.s2.p = p.bias.p = nullptr;
@@ -710,6 +793,10 @@ int ltx_op_linear_q8(ltx_ctx* c, const void* a, const int8_t* q, const void* sca
             if (c->op_pairs.bytes < np) c->op_pairs.alloc(np);
             sc.q = (uint32_t*)c->op_q.p;
             sc.pairs = (uint32_t*)c->op_pairs.p;
+            if (ltx::x4_shape(c, mode, M, N, K, K)) {
+                if (c->op_w16.bytes < 2 * nq) c->op_w16.alloc(2 * nq);
+                sc.w16 = c->op_w16.p;
+            }
         }
         ltx::linear_q8(c, a, q, scales, scale_f16, bias, y, out_f32, M, N, K, gelu, mode, sc, (hipStream_t)stream);
     })

@@ -88,6 +88,10 @@ struct ltx_ctx {
     // resident-K/V form of the ping-pong kernel (true) or its streaming form
     // (all kept for testing)
     bool gemm_dma = true;
+    // the four-wave 16-bit GEMM (int8 projections dequantised per forward):
+    // 0 never, 1 where its tiles fill the CUs (M >= 4,096 and no split-K),
+    // 2 wherever the shape allows (tests)
+    int gemm_x4 = 1;
     int num_cu = 256;             // compute units: the persistent GEMM's grid bound
     bool gemm_persistent = true;  // LDS-DMA GEMM: at most one workgroup per CU, looping over tiles
     bool attn_pp = true;
@@ -109,6 +113,7 @@ struct ltx_ctx {
     ltx::DevBuf range_ctr;  // range guard: 16-bit stores out of range (u64), see ltx_range_count
     ltx::DevBuf op_pairs;  // scale pairs of the last ltx_op_linear_q8 call (f16 scales)
     ltx::DevBuf op_q;      // its weights as bytes q + 128
+    ltx::DevBuf op_w16;    // and dequantised to 16 bits (four-wave GEMM)
     ltx::DevBuf blob_stage;  // device copy of the blob image of the last streaming upload
     ltx::DevBuf core_ws;   // conditioning MLP rows
     ltx::DevBuf tail_ws;   // normed rows of ltx_core_tail
@@ -155,7 +160,11 @@ float f16_bits_to_f32(uint16_t h);
 struct LinearScratch {
     uint32_t* q;
     uint32_t* pairs;
+    void* w16 = nullptr;  // N * K 16-bit weights for the four-wave GEMM, or NULL (the W8A16 kernel)
 };
+// Whether the four-wave 16-bit GEMM takes an M x N x K product with A rows of
+// lda elements (shape, 32-bit buffer offsets and the context's setting).
+bool x4_shape(const ltx_ctx* c, int mode, int M, int N, int K, int lda);
 // Shape and mode checks of the isolated int8 GEMM (throws Error), made before
 // any scratch is sized from N and K.
 void check_linear_q8(int M, int N, int K, int mode);

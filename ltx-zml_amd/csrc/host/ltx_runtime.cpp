@@ -178,11 +178,14 @@ int ltx_init(int device, ltx_ctx** out) {
         c->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
         // LTX_GEMM_GRID=tile: one workgroup per output tile instead of the
         // persistent grid of one per CU; LTX_GEMM_Q8=reg: the register-staged
-        // int8 GEMM everywhere; LTX_ATTN_VARIANT=w8: the any-length attention
+        // int8 GEMM everywhere; LTX_GEMM_X4=off / all: the four-wave 16-bit
+        // GEMM nowhere / wherever the shape allows; LTX_ATTN_VARIANT=w8: the any-length attention
         // everywhere, =pp: the streaming ping-pong attention also for 64-256
         // keys (the kernels each test exercises beside the defaults)
         if (const char* e = std::getenv("LTX_GEMM_GRID")) c->gemm_persistent = std::strcmp(e, "tile") != 0;
         if (const char* e = std::getenv("LTX_GEMM_Q8")) c->gemm_dma = std::strcmp(e, "reg") != 0;
+        if (const char* e = std::getenv("LTX_GEMM_X4"))
+            c->gemm_x4 = std::strcmp(e, "off") == 0 ? 0 : std::strcmp(e, "all") == 0 ? 2 : 1;
         if (const char* e = std::getenv("LTX_ATTN_VARIANT")) {
             c->attn_pp = std::strcmp(e, "w8") != 0;
             c->attn_kv = c->attn_pp && std::strcmp(e, "pp") != 0;

@@ -14,6 +14,7 @@
 #include "gemm_common.h"
 #include "gemm_q8.h"
 #include "gemm_w16.h"
+#include "gemm_x4.h"
 
 #define BM 256
 #define BN 256
@@ -215,6 +216,25 @@ W16_GEMM_KERNEL(ltx_gemm_w16dma_f16_qkv, _Float16, LTX_EPI_QKV)
 W16_GEMM_KERNEL(ltx_gemm_w16dma_bf16_store, __bf16, LTX_EPI_STORE)
 W16_GEMM_KERNEL(ltx_gemm_w16dma_bf16_resid, __bf16, LTX_EPI_RESID_GATE)
 W16_GEMM_KERNEL(ltx_gemm_w16dma_bf16_qkv, __bf16, LTX_EPI_QKV)
+
+// Four-wave 16-bit kernels (256 x 256 tiles, 16 x 16 x 32 MFMAs):
+// ltx_gemm_x4_{f16,bf16}_{store,resid,qkv}, and the per-forward
+// dequantisation of the int8 weights they take: ltx_gemm_dq16_{f16,bf16}
+// (fp16 scale pairs), _s32 (f32 scales).
+X4_GEMM_KERNEL(ltx_gemm_x4_f16_store, _Float16, LTX_EPI_STORE)
+X4_GEMM_KERNEL(ltx_gemm_x4_f16_resid, _Float16, LTX_EPI_RESID_GATE)
+X4_GEMM_KERNEL(ltx_gemm_x4_f16_qkv, _Float16, LTX_EPI_QKV)
+X4_GEMM_KERNEL(ltx_gemm_x4_bf16_store, __bf16, LTX_EPI_STORE)
+X4_GEMM_KERNEL(ltx_gemm_x4_bf16_resid, __bf16, LTX_EPI_RESID_GATE)
+X4_GEMM_KERNEL(ltx_gemm_x4_bf16_qkv, __bf16, LTX_EPI_QKV)
+extern "C" __global__ void __launch_bounds__(256) ltx_gemm_dq16_f16(const LtxDq16Args a) { dq16_body<_Float16, false>(a); }
+extern "C" __global__ void __launch_bounds__(256) ltx_gemm_dq16_f16_s32(const LtxDq16Args a) {
+    dq16_body<_Float16, true>(a);
+}
+extern "C" __global__ void __launch_bounds__(256) ltx_gemm_dq16_bf16(const LtxDq16Args a) { dq16_body<__bf16, false>(a); }
+extern "C" __global__ void __launch_bounds__(256) ltx_gemm_dq16_bf16_s32(const LtxDq16Args a) {
+    dq16_body<__bf16, true>(a);
+}
 
 // Gate logits (ltx/block.zig:238, 526, 564): glog[t][h] = a[t] . gw[h] + gb[h].
 // One wave per 32 token rows: 256 MFMAs over K = 4096, operands straight

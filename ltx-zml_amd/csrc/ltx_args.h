@@ -90,6 +90,20 @@ typedef struct {
     float* part;          // go to part [S][M][N] for ltx_gemm_reduce_* to finish with the epilogue
 } LtxGemmArgs;
 
+// Dequantisation of int8 projections into 16-bit weights for the four-wave
+// 16-bit GEMM: out[j] [N][K] = the W8A16 kernel's operands, from the bytes
+// q + 128 [N][K] and the scale words [K / 128][N]. Workgroups start[j] ..
+// start[j + 1] - 1 cover job j, 32 rows of one 128-k group each.
+#define LTX_DQ_JOBS 8
+typedef struct {
+    const uint8_t* q[LTX_DQ_JOBS];
+    const uint32_t* s2[LTX_DQ_JOBS];
+    void* out[LTX_DQ_JOBS];
+    int N[LTX_DQ_JOBS], K[LTX_DQ_JOBS];
+    int start[LTX_DQ_JOBS + 1];
+    int njobs;
+} LtxDq16Args;
+
 // Full-row qk RMSNorm (weighted, over all 4096 channels) + optional split-half
 // RoPE, writing 16-bit rows [rows][D] (head h at columns h * HD ..), the
 // layout of its input: every token's output is one contiguous 8 KB row.

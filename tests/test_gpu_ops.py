@@ -178,19 +178,30 @@ def test_linear_q8_onehot_extreme_f32_scales(ctx, mode, exp_range):
         assert ((want != 0) & (np.abs(want) < 6.1e-5)).sum() > 1000  # subnormal operands were exercised
 
 
-@pytest.mark.parametrize("variant", ["reg"])
+VARIANT_ENV = {"reg": ("LTX_GEMM_Q8", "reg"), "x4": ("LTX_GEMM_X4", "all")}
+
+
+@pytest.mark.parametrize("variant", ["reg", "x4"])
 def test_linear_q8_variants(monkeypatch, variant):
-    """The register-staged int8 GEMM (the kernel for bf16 weights and the
-    fallback of the LDS-DMA one), forced everywhere: the one-hot exactness
-    check and an f16-scale GEMM against the oracle."""
+    """Other GEMM kernels forced everywhere, in a context of their own:
+    - reg: the register-staged int8 GEMM (the fallback of the LDS-DMA one);
+    - x4: the four-wave 16-bit GEMM after the per-call dequantisation
+      (ltx_gemm_dq16_*), which the block uses from 4,096 rows.
+    The one-hot exactness check (every output one weight operand, bit for
+    bit: the dequantised operands, f16 and f32 scales, both operand types),
+    then GEMMs against the oracle: ragged M with a bias, and for x4 also GELU
+    into a 16-bit output in bf16 with f32 scales."""
     say(f"linear_q8 variant={variant}")
-    monkeypatch.setenv("LTX_GEMM_Q8", variant)
+    monkeypatch.setenv(*VARIANT_ENV[variant])
     c = rt.Context(0)
     try:
         for mode in ("f16", "bf16"):
             for sf32 in (False, True):
                 got, want = _onehot_case(c, 1024, 512, 1024, seed=9, mode=mode, sf32=sf32)
                 assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (mode, sf32)
+        if variant == "x4":
+            got, want = _onehot_case(c, 300, 256, 256, seed=10, mode="f16", sf32=False)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
         a, q, s, b = _gemm_case(300, 768, 4096, seed=11, scale_f16=True)
         y = torch.empty((300, 768), dtype=torch.float32, device="cuda")
         c.linear_q8(to16(a, torch.float16).cuda(), torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(),
@@ -198,6 +209,16 @@ def test_linear_q8_variants(monkeypatch, variant):
         torch.cuda.synchronize()
         want = f64(to16(a, torch.float16)) @ oracle.dequant(q, s).astype(np.float64).T + b
         assert oracle.rel_rms(f64(y), want) <= 1e-3
+        if variant == "x4":
+            a, q, s, b = _gemm_case(300, 512, 4096, seed=12, scale_f16=False)
+            da = to16(a, torch.bfloat16).cuda()
+            y = torch.empty((300, 512), dtype=torch.bfloat16, device="cuda")
+            c.linear_q8(da, torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(), torch.from_numpy(b).cuda(), y,
+                        mode=rt.MODE_BF16, gelu=True)
+            torch.cuda.synchronize()
+            z = f64(da) @ oracle.dequant(q, s).astype(np.float64).T + b
+            want = 0.5 * z * (1 + np.tanh(np.sqrt(2 / np.pi) * (z + 0.044715 * z ** 3)))
+            assert oracle.rel_rms(f64(y), want) <= 6e-3
     finally:
         c.close()
 

@@ -157,6 +157,53 @@ def test_unquantised_block_stages(ctx, block0_w16, mode, T, S):
         assert r["y"] <= 2e-3
 
 
+@pytest.fixture(scope="module")
+def ctx_x4():
+    """A context whose 16-bit GEMMs all take the four-wave kernel
+    (LTX_GEMM_X4=all; by default it runs from 4,096 rows), so that these small
+    T exercise it: the int8 projections dequantised per forward by
+    ltx_gemm_dq16_*, a ragged last row tile, and every epilogue (QKV split
+    with V^T, gated residual, GELU, 16-bit stores)."""
+    import os
+    old = os.environ.get("LTX_GEMM_X4")
+    os.environ["LTX_GEMM_X4"] = "all"
+    try:
+        c = rt.Context(0)
+    finally:
+        if old is None:
+            del os.environ["LTX_GEMM_X4"]
+        else:
+            os.environ["LTX_GEMM_X4"] = old
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("weights", ["int8", "bf16"])
+@pytest.mark.parametrize("T,S", [(256, 64), (250, 40)])
+@pytest.mark.parametrize("mode", ["f16", "bf16"])
+def test_block_stages_x4(ctx_x4, block0, block0_w16, mode, T, S, weights):
+    """The block with every projection on the four-wave 16-bit GEMM: int8
+    weights (dequantised for the forward) and the unquantised block, every
+    stage against the oracle under the gates of test_block_stages."""
+    say(f"block stages four-wave GEMM mode={mode} T={T} S={S} weights={weights}")
+    bt = block0 if weights == "int8" else block0_w16
+    inp = synth.make_inputs(T, S, sigma=0.7)
+    cos, sin = rt.rope_tables(inp["grid"])
+    key = ("b0" if weights == "int8" else "w16", T, S)
+    if key not in _CACHE:
+        _CACHE[key] = oracle.block_forward(bt, inp, cos, sin, chunk=16 if T % 16 == 0 else 0, stages=True)
+    want, wst = _CACHE[key]
+    w = ctx_x4.upload(bt)
+    y = forward(ctx_x4, w, inp, cos, sin, mode)
+    g = gpu_stages(ctx_x4, mode, T, S)
+    w.free()
+    r = compare_stages(g, y, want, wst, inp["x"].astype(np.float64))
+    say("  " + " ".join(f"{k}={v:.2e}" for k, v in r.items()))
+    bad = {k: v for k, v in r.items() if not v <= GATE[mode]}
+    assert not bad, f"stages over the {GATE[mode]:.0e} gate: {bad}"
+    assert r["y"] <= 2e-3, r
+
+
 @pytest.mark.parametrize("mode", ["f16", "f32"])
 def test_block_closed_form(ctx, block0, mode):
     """The special case of tests/blockcases.py on the GPU: every token's
