@@ -93,62 +93,85 @@ __device__ __forceinline__ void gemm_epilogue(const LtxGemmArgs& a, const f32x16
 // 32-row block i (row r of the block at patch[r * LD + column]), so kernels
 // with other MFMA layouts share everything after it; gemm_epilogue_lds below
 // is the form for NI x NJ blocks of 32 x 32.
-template <typename T, int EPI, int NI, int NJ, typename Fill>
-__device__ __forceinline__ void gemm_epilogue_patch(const LtxGemmArgs& a, Fill fill, float* patch, int mw, int nw,
-                                                    int n0) {
+//
+// The body is compiled per output form (OUT: 0 16-bit rows, 1 f32 rows, 2
+// V^T), GELU and whether every row of the wave's tile is inside M (FULL, and M
+// a multiple of 8): with no branch per row and the per-column values (bias,
+// gate shift) loaded once before the blocks, no load of a later block waits
+// behind the stores of an earlier one. (Written with a branch per row and the
+// bias loaded per block, the wait-insertion pass put a vmcnt(0), which counts
+// the block's stores too, before every patch read.)
+template <typename T, int EPI, int NI, int NJ, int OUT, bool GELU, bool FULL, typename Fill>
+__device__ __forceinline__ void gemm_epilogue_body(const LtxGemmArgs& a, Fill fill, float* patch, int mw, int nw) {
     constexpr int WN = 32 * NJ, LD = WN + 8;
-    const int lane = threadIdx.x & 63;
-    const bool vt = EPI == LTX_EPI_QKV && n0 >= a.nsplit;
-    const bool f32out = EPI == LTX_EPI_RESID_GATE || (EPI == LTX_EPI_STORE && a.out_f32);
+    const int lane = opaque_tid() & 63;
     const int ldo = EPI == LTX_EPI_QKV ? a.nsplit : a.ldo;  // 16-bit rows: q | k [M][nsplit] or [M][ldo]
     unsigned bad = 0;  // 16-bit stores out of range (range guard)
-    // gated residual: lane rows r0 + RRPP p of each 32-row block, 4 columns
-    // each. The timestep rows of block i + 1 are loaded with block i's
-    // loads, so that a block's gate-row loads do not wait out a round trip
-    // for them.
+    // f32 rows (and the gated residual): 4 columns a lane, RPP rows a pass
     constexpr int RLPR = WN / 4, RRPP = 64 / RLPR, RNP = 32 / RRPP;
-    constexpr int TNP = EPI == LTX_EPI_RESID_GATE ? RNP : 1;
-    int tixn[TNP];
-    if (EPI == LTX_EPI_RESID_GATE)
+    // 16-bit rows: 8 columns a lane
+    constexpr int HLPR = WN / 8, HRPP = 64 / HLPR;
+    constexpr bool RES = EPI == LTX_EPI_RESID_GATE;
+    constexpr int TNP = RES ? RNP : 1;
+    // per-column values, loaded once for the wave's tile
+    f32x4 cb0 = {0, 0, 0, 0}, cb1 = {0, 0, 0, 0}, gs = {0, 0, 0, 0};
+    float bn[OUT == 2 ? WN / 16 : 1];
+    if (OUT == 0) {
+        const int n = nw + 8 * (lane % HLPR);
+        if (a.bias) {
+            cb0 = *(const f32x4*)(a.bias + n);
+            cb1 = *(const f32x4*)(a.bias + n + 4);
+        }
+    } else if (OUT == 1) {
+        const int n = nw + 4 * (lane % RLPR);
+        if (a.bias) cb0 = *(const f32x4*)(a.bias + n);
+        if (RES) gs = *(const f32x4*)(a.ada.sst + (size_t)a.igate * LTX_D + n);
+    } else {
 #pragma unroll
-        for (int p = 0; p < TNP; p++) tixn[p] = ada_row(a.ada, min(mw + lane / RLPR + RRPP * p, a.M - 1));
+        for (int p = 0; p < WN / 16; p++) bn[p] = a.bias ? a.bias[nw + 16 * p + (lane >> 2)] : 0.0f;
+    }
+    auto row = [&](int m) { return FULL ? m : min(m, a.M - 1); };
+    // gated residual: lane rows r0 + RRPP p of each 32-row block. The
+    // timestep rows of block i + 1 are looked up with block i's loads, so
+    // that a block's gate-row loads do not wait out a round trip for them.
+    int tixn[TNP];
+    if (RES)
+#pragma unroll
+        for (int p = 0; p < TNP; p++) tixn[p] = ada_row(a.ada, row(mw + lane / RLPR + RRPP * p));
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         const int mb = mw + 32 * i;
         // this block's residual rows and gate rows are loaded before
-        // anything is stored (the stores could alias them for the compiler,
-        // which would otherwise wait out one load round trip per row group)
+        // anything is stored
         f32x4 rs[TNP], gt[TNP];
-        if (EPI == LTX_EPI_RESID_GATE) {
-            const int c4 = 4 * (lane % RLPR), r0 = lane / RLPR;
-            const int n = nw + c4;
+        if (RES) {
+            const int n = nw + 4 * (lane % RLPR), r0 = lane / RLPR;
 #pragma unroll
             for (int p = 0; p < RNP; p++) {
-                const int m = min(mb + r0 + RRPP * p, a.M - 1);
+                const int m = row(mb + r0 + RRPP * p);
                 rs[p] = __builtin_nontemporal_load((const f32x4*)(a.resid + (size_t)m * a.ldo + n));
                 gt[p] = *(const f32x4*)(a.ada.tstab + ((size_t)tixn[p] * 9 + a.igate) * LTX_D + n);
             }
             if (i + 1 < NI)
 #pragma unroll
-                for (int p = 0; p < RNP; p++) tixn[p] = ada_row(a.ada, min(mb + 32 + r0 + RRPP * p, a.M - 1));
+                for (int p = 0; p < RNP; p++) tixn[p] = ada_row(a.ada, row(mb + 32 + r0 + RRPP * p));
         }
         fill(i, patch, LD);
-        if (vt) {
+        if (OUT == 2) {
             // V^T [c][m]: 4 lanes cover one column's 32 rows (64 contiguous bytes)
             const int rg = lane & 3;
 #pragma unroll
             for (int p = 0; p < WN / 16; p++) {
                 const int cc = 16 * p + (lane >> 2);
-                const int n = nw + cc, c = n - a.nsplit;
-                const float bn = a.bias ? a.bias[n] : 0.0f;
+                const int c = nw + cc - a.nsplit;
                 float v[8];
 #pragma unroll
-                for (int e = 0; e < 8; e++) v[e] = patch[(8 * rg + e) * LD + cc] + bn;
+                for (int e = 0; e < 8; e++) v[e] = patch[(8 * rg + e) * LD + cc] + bn[p];
                 const int m = mb + 8 * rg;
                 uint16_t* dst = (uint16_t*)a.out2 + (size_t)c * a.M + m;
 #pragma unroll
-                for (int e = 0; e < 8; e++) bad += m + e < a.M ? out_of_range<T>(v[e]) : 0u;
-                if ((a.M & 7) == 0 && m + 8 <= a.M) {
+                for (int e = 0; e < 8; e++) bad += (FULL || m + e < a.M) ? out_of_range<T>(v[e]) : 0u;
+                if (FULL || ((a.M & 7) == 0 && m + 8 <= a.M)) {
                     __builtin_nontemporal_store(u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]),
                                                       pack2<T>(v[4], v[5]), pack2<T>(v[6], v[7])},
                                                 (u32x4*)dst);
@@ -158,20 +181,16 @@ __device__ __forceinline__ void gemm_epilogue_patch(const LtxGemmArgs& a, Fill f
                         if (m + e < a.M) dst[e] = Op<T>::bits(v[e]);
                 }
             }
-        } else if (f32out) {
-            constexpr int LPR = WN / 4, RPP = 64 / LPR;  // lanes per row, rows per pass
-            const int c4 = 4 * (lane % LPR), r0 = lane / LPR;
+        } else if (OUT == 1) {
+            const int c4 = 4 * (lane % RLPR), r0 = lane / RLPR;
             const int n = nw + c4;
-            f32x4 bias = a.bias ? *(const f32x4*)(a.bias + n) : f32x4{0, 0, 0, 0};
-            f32x4 gs = {0, 0, 0, 0};
-            if (EPI == LTX_EPI_RESID_GATE) gs = *(const f32x4*)(a.ada.sst + (size_t)a.igate * LTX_D + n);
 #pragma unroll
-            for (int p = 0; p < 32 / RPP; p++) {
-                const int rr = r0 + RPP * p, m = mb + rr;
-                if (m >= a.M) continue;
-                f32x4 v = *(const f32x4*)(patch + rr * LD + c4) + bias;
-                if (EPI == LTX_EPI_STORE) {
-                    if (a.gelu) v = f32x4{gelu_tanh(v[0]), gelu_tanh(v[1]), gelu_tanh(v[2]), gelu_tanh(v[3])};
+            for (int p = 0; p < RNP; p++) {
+                const int rr = r0 + RRPP * p, m = mb + rr;
+                if (!FULL && m >= a.M) continue;
+                f32x4 v = *(const f32x4*)(patch + rr * LD + c4) + cb0;
+                if (!RES) {
+                    if (GELU) v = f32x4{gelu_tanh(v[0]), gelu_tanh(v[1]), gelu_tanh(v[2]), gelu_tanh(v[3])};
                     *(f32x4*)((float*)a.out + (size_t)m * a.ldo + n) = v;
                 } else {  // gated residual
                     const size_t o = (size_t)m * a.ldo + n;
@@ -179,21 +198,15 @@ __device__ __forceinline__ void gemm_epilogue_patch(const LtxGemmArgs& a, Fill f
                 }
             }
         } else {  // 16-bit rows: 8 columns a lane
-            constexpr int LPR = WN / 8, RPP = 64 / LPR;
-            const int c8 = 8 * (lane % LPR), r0 = lane / LPR;
+            const int c8 = 8 * (lane % HLPR), r0 = lane / HLPR;
             const int n = nw + c8;
-            f32x4 b0 = {0, 0, 0, 0}, b1 = {0, 0, 0, 0};
-            if (a.bias) {
-                b0 = *(const f32x4*)(a.bias + n);
-                b1 = *(const f32x4*)(a.bias + n + 4);
-            }
 #pragma unroll
-            for (int p = 0; p < 32 / RPP; p++) {
-                const int rr = r0 + RPP * p, m = mb + rr;
-                if (m >= a.M) continue;
-                f32x4 v0 = *(const f32x4*)(patch + rr * LD + c8) + b0;
-                f32x4 v1 = *(const f32x4*)(patch + rr * LD + c8 + 4) + b1;
-                if (EPI == LTX_EPI_STORE && a.gelu) {
+            for (int p = 0; p < 32 / HRPP; p++) {
+                const int rr = r0 + HRPP * p, m = mb + rr;
+                if (!FULL && m >= a.M) continue;
+                f32x4 v0 = *(const f32x4*)(patch + rr * LD + c8) + cb0;
+                f32x4 v1 = *(const f32x4*)(patch + rr * LD + c8 + 4) + cb1;
+                if (GELU) {
                     v0 = f32x4{gelu_tanh(v0[0]), gelu_tanh(v0[1]), gelu_tanh(v0[2]), gelu_tanh(v0[3])};
                     v1 = f32x4{gelu_tanh(v1[0]), gelu_tanh(v1[1]), gelu_tanh(v1[2]), gelu_tanh(v1[3])};
                 }
@@ -208,10 +221,45 @@ __device__ __forceinline__ void gemm_epilogue_patch(const LtxGemmArgs& a, Fill f
     range_report(a.sat, bad);
 }
 
+template <typename T, int EPI, int NI, int NJ, int OUT, bool GELU, typename Fill>
+__device__ __forceinline__ void gemm_epilogue_rows(const LtxGemmArgs& a, Fill fill, float* patch, int mw, int nw) {
+    if (mw + 32 * NI <= a.M && (a.M & 7) == 0)
+        gemm_epilogue_body<T, EPI, NI, NJ, OUT, GELU, true>(a, fill, patch, mw, nw);
+    else
+        gemm_epilogue_body<T, EPI, NI, NJ, OUT, GELU, false>(a, fill, patch, mw, nw);
+}
+
+// SF: the STORE epilogue's form fixed at compile time (bit 0 GELU, bit 1 f32
+// output), or -1 to take a.gelu and a.out_f32 at run time.
+template <typename T, int EPI, int NI, int NJ, typename Fill, int SF = -1>
+__device__ __forceinline__ void gemm_epilogue_patch(const LtxGemmArgs& a, Fill fill, float* patch, int mw, int nw,
+                                                    int n0) {
+    if (EPI == LTX_EPI_STORE && SF >= 0) {
+        gemm_epilogue_rows<T, EPI, NI, NJ, (SF & 2) ? 1 : 0, (SF & 1) != 0>(a, fill, patch, mw, nw);
+    } else if (EPI == LTX_EPI_QKV) {
+        if (n0 >= a.nsplit)
+            gemm_epilogue_rows<T, EPI, NI, NJ, 2, false>(a, fill, patch, mw, nw);
+        else
+            gemm_epilogue_rows<T, EPI, NI, NJ, 0, false>(a, fill, patch, mw, nw);
+    } else if (EPI == LTX_EPI_RESID_GATE) {
+        gemm_epilogue_rows<T, EPI, NI, NJ, 1, false>(a, fill, patch, mw, nw);
+    } else if (a.out_f32) {
+        if (a.gelu)
+            gemm_epilogue_rows<T, EPI, NI, NJ, 1, true>(a, fill, patch, mw, nw);
+        else
+            gemm_epilogue_rows<T, EPI, NI, NJ, 1, false>(a, fill, patch, mw, nw);
+    } else {
+        if (a.gelu)
+            gemm_epilogue_rows<T, EPI, NI, NJ, 0, true>(a, fill, patch, mw, nw);
+        else
+            gemm_epilogue_rows<T, EPI, NI, NJ, 0, false>(a, fill, patch, mw, nw);
+    }
+}
+
 template <typename T, int EPI, int NI, int NJ>
 __device__ __forceinline__ void gemm_epilogue_lds(const LtxGemmArgs& a, const f32x16 (&acc)[NI][NJ], float* patch,
                                                   int mw, int nw, int n0) {
-    const int lane = threadIdx.x & 63;
+    const int lane = opaque_tid() & 63;
     gemm_epilogue_patch<T, EPI, NI, NJ>(
         a,
         [&](int i, float* p, int LD) {

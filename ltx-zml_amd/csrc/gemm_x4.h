@@ -55,7 +55,23 @@ __device__ __forceinline__ uint8_t* x4_stage_b() {
 // s_waitcnt: vmcnt(0) and lgkmcnt(0)
 #define X4_WAIT_ALL0 (7 << 4)
 
-template <typename T, int EPI>
+// A per-lane (v) or wave-uniform (s) offset through an empty volatile asm, at
+// the point of use: the LDS addresses derived from it are formed there (one
+// add, the rest in the instructions' offset fields) instead of being hoisted
+// out of the tile loop as one register per fragment and DMA slice (which ran
+// out of registers and spilled around the epilogue).
+__device__ __forceinline__ uint32_t x4_vofs(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+__device__ __forceinline__ int x4_sofs(int x) {
+    asm volatile("" : "+s"(x));
+    return x;
+}
+
+// SF: the STORE epilogue's form (bit 0 GELU, bit 1 f32 output), one kernel
+// each, so that a kernel holds only the epilogue it runs.
+template <typename T, int EPI, int SF = 0>
 struct X4Gemm {
     typedef typename Op<T>::v8 V8;
     const LtxGemmArgs& a;
@@ -76,18 +92,19 @@ struct X4Gemm {
 
     template <int RS, int RSTEP>
     __device__ __forceinline__ void read_all(u32x4 (&ya)[8], u32x4 (&yb)[8]) {
-        const uint8_t* sa = x4_stage_a<RS>();
-        const uint8_t* sb = x4_stage_b<RS>();
+        const uint8_t* sa = x4_stage_a<RS>() + x4_vofs(offa[RSTEP]);
+        const uint8_t* sb = x4_stage_b<RS>() + x4_vofs(offb[RSTEP]);
 #pragma unroll
-        for (int i = 0; i < 8; i++) ya[i] = *(const u32x4*)(sa + offa[RSTEP] + 2048 * i);
+        for (int i = 0; i < 8; i++) ya[i] = *(const u32x4*)(sa + 2048 * i);
 #pragma unroll
-        for (int j = 0; j < 8; j++) yb[j] = *(const u32x4*)(sb + offb[RSTEP] + 2048 * j);
+        for (int j = 0; j < 8; j++) yb[j] = *(const u32x4*)(sb + 2048 * j);
     }
 
     template <int DS>
     __device__ __forceinline__ void dma(int k) {
-        uint8_t* da = x4_stage_a<DS>() + lw;
-        uint8_t* db = x4_stage_b<DS>() + lw;
+        const int l = x4_sofs(lw);
+        uint8_t* da = x4_stage_a<DS>() + l;
+        uint8_t* db = x4_stage_b<DS>() + l;
 #pragma unroll
         for (int i = 0; i < 8; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_, (lds_vptr)(da + 1024 * i), 16, ga[i], k * 128, 0, 0);
@@ -111,10 +128,11 @@ struct X4Gemm {
     template <int RS, int RSTEP, int DS, bool DMA>
     __device__ __forceinline__ void region(const u32x4 (&xa)[8], const u32x4 (&xb)[8], u32x4 (&ya)[8],
                                            u32x4 (&yb)[8], int kd) {
-        const uint8_t* sa = x4_stage_a<RS>();
-        const uint8_t* sb = x4_stage_b<RS>();
-        uint8_t* da = x4_stage_a<DS>() + lw;
-        uint8_t* db = x4_stage_b<DS>() + lw;
+        const uint8_t* sa = x4_stage_a<RS>() + x4_vofs(offa[RSTEP]);
+        const uint8_t* sb = x4_stage_b<RS>() + x4_vofs(offb[RSTEP]);
+        const int l = DMA ? x4_sofs(lw) : 0;
+        uint8_t* da = x4_stage_a<DS>() + l;
+        uint8_t* db = x4_stage_b<DS>() + l;
 #pragma unroll
         for (int m = 0; m < 64; m++) {
             mfma(xa[m >> 3], xb[m & 7], acc[m >> 3][m & 7]);
@@ -122,11 +140,11 @@ struct X4Gemm {
                 const int g = m / 3;
                 __builtin_amdgcn_sched_barrier(0);
                 if (g == 0)
-                    ya[0] = *(const u32x4*)(sa + offa[RSTEP]);
+                    ya[0] = *(const u32x4*)sa;
                 else if (g <= 8)
-                    yb[g - 1] = *(const u32x4*)(sb + offb[RSTEP] + 2048 * (g - 1));
+                    yb[g - 1] = *(const u32x4*)(sb + 2048 * (g - 1));
                 else
-                    ya[g - 8] = *(const u32x4*)(sa + offa[RSTEP] + 2048 * (g - 8));
+                    ya[g - 8] = *(const u32x4*)(sa + 2048 * (g - 8));
                 if (DMA) {
                     if (g < 8)
                         __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_, (lds_vptr)(da + 1024 * g), 16, ga[g], kd * 128,
@@ -215,27 +233,27 @@ struct X4Gemm {
             mfma_all(fa1, fb1);  // tile nk - 1, step 1
             meet();
             // every wave has passed the last barrier: the stages are free
-            gemm_epilogue_patch<T, EPI, 4, 4>(
-                a,
-                [&](int b, float* p, int LD) {
+            const int el = opaque_tid() & 63;
+            auto fill = [&](int b, float* p, int LD) {
 #pragma unroll
-                    for (int e = 0; e < 2; e++)
+                for (int e = 0; e < 2; e++)
 #pragma unroll
-                        for (int j = 0; j < 8; j++)
+                    for (int j = 0; j < 8; j++)
 #pragma unroll
-                            for (int r = 0; r < 4; r++)
-                                p[(16 * e + 4 * (lane >> 4) + r) * LD + 16 * j + (lane & 15)] = acc[2 * b + e][j][r];
-                },
-                (float*)patch, m0 + wm, n0 + wn, n0);
+                        for (int r = 0; r < 4; r++)
+                            p[(16 * e + 4 * (el >> 4) + r) * LD + 16 * j + (el & 15)] = acc[2 * b + e][j][r];
+            };
+            gemm_epilogue_patch<T, EPI, 4, 4, decltype(fill), EPI == LTX_EPI_STORE ? SF : -1>(a, fill, (float*)patch,
+                                                                                              m0 + wm, n0 + wn, n0);
             // every patch has been read back before the next tile's DMA
             meet();
         }
     }
 };
 
-#define X4_GEMM_KERNEL(NAME, T_, EPI_)                                               \
+#define X4_GEMM_KERNEL(NAME, T_, EPI_, SF_)                                          \
     extern "C" __global__ void __launch_bounds__(256, 1) NAME(const LtxGemmArgs a) { \
-        X4Gemm<T_, EPI_> k(a);                                                       \
+        X4Gemm<T_, EPI_, SF_> k(a);                                                  \
         k.run();                                                                     \
     }
 

@@ -204,7 +204,8 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
             g.b = wb;
             g.scales = nullptr;
             g.ksplit = 1;
-            std::snprintf(name, sizeof(name), "ltx_gemm_x4_%s_%s", msuffix(mode), es);
+            std::snprintf(name, sizeof(name), "ltx_gemm_x4_%s_%s%s%s", msuffix(mode), es,
+                          epi == LTX_EPI_STORE && g.out_f32 ? "32" : "", epi == LTX_EPI_STORE && g.gelu ? "_gelu" : "");
             const int nitems = g.tiles_m * g.tiles_n;
             c->launch(name, c->gemm_persistent ? std::min(nitems, c->num_cu) : nitems, 1, 1, 256, &g, st, label);
             return;

@@ -218,15 +218,22 @@ W16_GEMM_KERNEL(ltx_gemm_w16dma_bf16_resid, __bf16, LTX_EPI_RESID_GATE)
 W16_GEMM_KERNEL(ltx_gemm_w16dma_bf16_qkv, __bf16, LTX_EPI_QKV)
 
 // Four-wave 16-bit kernels (256 x 256 tiles, 16 x 16 x 32 MFMAs):
-// ltx_gemm_x4_{f16,bf16}_{store,resid,qkv}, and the per-forward
-// dequantisation of the int8 weights they take: ltx_gemm_dq16_{f16,bf16}
-// (fp16 scale pairs), _s32 (f32 scales).
-X4_GEMM_KERNEL(ltx_gemm_x4_f16_store, _Float16, LTX_EPI_STORE)
-X4_GEMM_KERNEL(ltx_gemm_x4_f16_resid, _Float16, LTX_EPI_RESID_GATE)
-X4_GEMM_KERNEL(ltx_gemm_x4_f16_qkv, _Float16, LTX_EPI_QKV)
-X4_GEMM_KERNEL(ltx_gemm_x4_bf16_store, __bf16, LTX_EPI_STORE)
-X4_GEMM_KERNEL(ltx_gemm_x4_bf16_resid, __bf16, LTX_EPI_RESID_GATE)
-X4_GEMM_KERNEL(ltx_gemm_x4_bf16_qkv, __bf16, LTX_EPI_QKV)
+// ltx_gemm_x4_{f16,bf16}_{store,store_gelu,store32,store32_gelu,resid,qkv}
+// (store32: f32 output), and the per-forward dequantisation of the int8
+// weights they take: ltx_gemm_dq16_{f16,bf16} (fp16 scale pairs), _s32 (f32
+// scales).
+X4_GEMM_KERNEL(ltx_gemm_x4_f16_store, _Float16, LTX_EPI_STORE, 0)
+X4_GEMM_KERNEL(ltx_gemm_x4_f16_store_gelu, _Float16, LTX_EPI_STORE, 1)
+X4_GEMM_KERNEL(ltx_gemm_x4_f16_store32, _Float16, LTX_EPI_STORE, 2)
+X4_GEMM_KERNEL(ltx_gemm_x4_f16_store32_gelu, _Float16, LTX_EPI_STORE, 3)
+X4_GEMM_KERNEL(ltx_gemm_x4_f16_resid, _Float16, LTX_EPI_RESID_GATE, 0)
+X4_GEMM_KERNEL(ltx_gemm_x4_f16_qkv, _Float16, LTX_EPI_QKV, 0)
+X4_GEMM_KERNEL(ltx_gemm_x4_bf16_store, __bf16, LTX_EPI_STORE, 0)
+X4_GEMM_KERNEL(ltx_gemm_x4_bf16_store_gelu, __bf16, LTX_EPI_STORE, 1)
+X4_GEMM_KERNEL(ltx_gemm_x4_bf16_store32, __bf16, LTX_EPI_STORE, 2)
+X4_GEMM_KERNEL(ltx_gemm_x4_bf16_store32_gelu, __bf16, LTX_EPI_STORE, 3)
+X4_GEMM_KERNEL(ltx_gemm_x4_bf16_resid, __bf16, LTX_EPI_RESID_GATE, 0)
+X4_GEMM_KERNEL(ltx_gemm_x4_bf16_qkv, __bf16, LTX_EPI_QKV, 0)
 extern "C" __global__ void __launch_bounds__(256) ltx_gemm_dq16_f16(const LtxDq16Args a) { dq16_body<_Float16, false>(a); }
 extern "C" __global__ void __launch_bounds__(256) ltx_gemm_dq16_f16_s32(const LtxDq16Args a) {
     dq16_body<_Float16, true>(a);

@@ -102,6 +102,18 @@ __device__ __forceinline__ void range_report(unsigned long long* sat, unsigned n
     if (n && sat) atomicAdd(sat, (unsigned long long)n);
 }
 
+// threadIdx.x through an empty volatile asm: values derived from it cannot be
+// hoisted out of the loop that contains the call. Epilogues inside a
+// persistent tile loop take their lane from it, so that their address
+// arithmetic is recomputed per tile instead of living across the main loop,
+// where registers are short (the hoisted values were spilled and their
+// reloads waited behind the tile's stores).
+__device__ __forceinline__ int opaque_tid() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 // Pack two f32 into two 16-bit lanes of one dword (lo = a).
 template <typename T>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
