@@ -96,12 +96,17 @@ __device__ __forceinline__ void gemm_epilogue(const LtxGemmArgs& a, const f32x16
 //
 // The body is compiled per output form (OUT: 0 16-bit rows, 1 f32 rows, 2
 // V^T), GELU and whether every row of the wave's tile is inside M (FULL, and M
-// a multiple of 8): with no branch per row and the per-column values (bias,
-// gate shift) loaded once before the blocks, no load of a later block waits
-// behind the stores of an earlier one. (Written with a branch per row and the
-// bias loaded per block, the wait-insertion pass put a vmcnt(0), which counts
-// the block's stores too, before every patch read.)
-template <typename T, int EPI, int NI, int NJ, int OUT, bool GELU, bool FULL, typename Fill>
+// a multiple of 8), and the per-column values (bias, gate shift) are loaded
+// once before the blocks. On full tiles the stores are issued in batches
+// from registers that nothing reuses before they have gone out: the 16-bit
+// outputs of HOLD blocks (the whole wave tile where registers allow) are
+// formed first and then stored, the f32 rows block by block. (Stored pass by pass, each patch read reused the
+// registers of the store before it, and the wait-insertion pass made the
+// read wait for that store to complete: 32 store round trips a tile.) The
+// range guard takes each block's largest |value| (v_maximum3, which
+// propagates NaN: half an instruction per value) and counts the block's
+// values one by one from the patch only when that exceeds the type's range.
+template <typename T, int EPI, int NI, int NJ, int OUT, bool GELU, bool FULL, int HOLD, typename Fill>
 __device__ __forceinline__ void gemm_epilogue_body(const LtxGemmArgs& a, Fill fill, float* patch, int mw, int nw) {
     constexpr int WN = 32 * NJ, LD = WN + 8;
     const int lane = opaque_tid() & 63;
@@ -110,12 +115,15 @@ __device__ __forceinline__ void gemm_epilogue_body(const LtxGemmArgs& a, Fill fi
     // f32 rows (and the gated residual): 4 columns a lane, RPP rows a pass
     constexpr int RLPR = WN / 4, RRPP = 64 / RLPR, RNP = 32 / RRPP;
     // 16-bit rows: 8 columns a lane
-    constexpr int HLPR = WN / 8, HRPP = 64 / HLPR;
+    constexpr int HLPR = WN / 8, HRPP = 64 / HLPR, HNP = 32 / HRPP;
+    // V^T: 4 lanes cover one column's 32 rows (64 contiguous bytes)
+    constexpr int VNP = WN / 16;
     constexpr bool RES = EPI == LTX_EPI_RESID_GATE;
     constexpr int TNP = RES ? RNP : 1;
+    constexpr int BNP = OUT == 0 ? HNP : OUT == 2 ? VNP : 1;  // batched 16-bit stores per block
     // per-column values, loaded once for the wave's tile
     f32x4 cb0 = {0, 0, 0, 0}, cb1 = {0, 0, 0, 0}, gs = {0, 0, 0, 0};
-    float bn[OUT == 2 ? WN / 16 : 1];
+    float bn[OUT == 2 ? VNP : 1];
     if (OUT == 0) {
         const int n = nw + 8 * (lane % HLPR);
         if (a.bias) {
@@ -128,9 +136,10 @@ __device__ __forceinline__ void gemm_epilogue_body(const LtxGemmArgs& a, Fill fi
         if (RES) gs = *(const f32x4*)(a.ada.sst + (size_t)a.igate * LTX_D + n);
     } else {
 #pragma unroll
-        for (int p = 0; p < WN / 16; p++) bn[p] = a.bias ? a.bias[nw + 16 * p + (lane >> 2)] : 0.0f;
+        for (int p = 0; p < VNP; p++) bn[p] = a.bias ? a.bias[nw + 16 * p + (lane >> 2)] : 0.0f;
     }
     auto row = [&](int m) { return FULL ? m : min(m, a.M - 1); };
+    auto act = [&](float v) { return GELU ? gelu_tanh(v) : v; };
     // gated residual: lane rows r0 + RRPP p of each 32-row block. The
     // timestep rows of block i + 1 are looked up with block i's loads, so
     // that a block's gate-row loads do not wait out a round trip for them.
@@ -138,6 +147,8 @@ __device__ __forceinline__ void gemm_epilogue_body(const LtxGemmArgs& a, Fill fi
     if (RES)
 #pragma unroll
         for (int p = 0; p < TNP; p++) tixn[p] = ada_row(a.ada, row(mw + lane / RLPR + RRPP * p));
+    static_assert(NI % HOLD == 0, "HOLD divides the blocks");
+    u32x4 ob[HOLD][BNP];  // full tiles: the 16-bit outputs of HOLD blocks, stored together
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         const int mb = mw + 32 * i;
@@ -158,50 +169,76 @@ __device__ __forceinline__ void gemm_epilogue_body(const LtxGemmArgs& a, Fill fi
         }
         fill(i, patch, LD);
         if (OUT == 2) {
-            // V^T [c][m]: 4 lanes cover one column's 32 rows (64 contiguous bytes)
             const int rg = lane & 3;
+            float mx = 0.0f;
 #pragma unroll
-            for (int p = 0; p < WN / 16; p++) {
+            for (int p = 0; p < VNP; p++) {
                 const int cc = 16 * p + (lane >> 2);
                 const int c = nw + cc - a.nsplit;
                 float v[8];
 #pragma unroll
                 for (int e = 0; e < 8; e++) v[e] = patch[(8 * rg + e) * LD + cc] + bn[p];
                 const int m = mb + 8 * rg;
-                uint16_t* dst = (uint16_t*)a.out2 + (size_t)c * a.M + m;
+                const u32x4 pk = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
+                                  pack2<T>(v[6], v[7])};
+                if (FULL) {
+                    ob[i % HOLD][p] = pk;
 #pragma unroll
-                for (int e = 0; e < 8; e++) bad += (FULL || m + e < a.M) ? out_of_range<T>(v[e]) : 0u;
-                if (FULL || ((a.M & 7) == 0 && m + 8 <= a.M)) {
-                    __builtin_nontemporal_store(u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]),
-                                                      pack2<T>(v[4], v[5]), pack2<T>(v[6], v[7])},
-                                                (u32x4*)dst);
+                    for (int e = 0; e < 8; e++) mx = __builtin_elementwise_maximum(mx, __builtin_fabsf(v[e]));
                 } else {
+                    uint16_t* dst = (uint16_t*)a.out2 + (size_t)c * a.M + m;
 #pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        if (m + e < a.M) dst[e] = Op<T>::bits(v[e]);
+                    for (int e = 0; e < 8; e++) bad += m + e < a.M ? out_of_range<T>(v[e]) : 0u;
+                    if ((a.M & 7) == 0 && m + 8 <= a.M) {
+                        __builtin_nontemporal_store(pk, (u32x4*)dst);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; e++)
+                            if (m + e < a.M) dst[e] = Op<T>::bits(v[e]);
+                    }
                 }
             }
+            if (FULL && !(mx <= RangeMax<T>::v))  // rare: count this block's values from the patch
+#pragma unroll
+                for (int p = 0; p < VNP; p++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        bad += out_of_range<T>(patch[(8 * rg + e) * LD + 16 * p + (lane >> 2)] + bn[p]);
         } else if (OUT == 1) {
             const int c4 = 4 * (lane % RLPR), r0 = lane / RLPR;
             const int n = nw + c4;
+            // the block's rows formed first, then stored (HOLD > 1: the
+            // kernels with registers to spare), or row by row
+            constexpr int BO = FULL && HOLD > 1 ? RNP : 1;
+            f32x4 o[BO];
 #pragma unroll
             for (int p = 0; p < RNP; p++) {
-                const int rr = r0 + RRPP * p, m = mb + rr;
-                if (!FULL && m >= a.M) continue;
+                const int rr = r0 + RRPP * p;
                 f32x4 v = *(const f32x4*)(patch + rr * LD + c4) + cb0;
                 if (!RES) {
                     if (GELU) v = f32x4{gelu_tanh(v[0]), gelu_tanh(v[1]), gelu_tanh(v[2]), gelu_tanh(v[3])};
-                    *(f32x4*)((float*)a.out + (size_t)m * a.ldo + n) = v;
+                    o[p % BO] = v;
                 } else {  // gated residual
-                    const size_t o = (size_t)m * a.ldo + n;
-                    __builtin_nontemporal_store(rs[p] + v * (gt[p] + gs), (f32x4*)((float*)a.out + o));
+                    o[p % BO] = rs[p] + v * (gt[p] + gs);
+                }
+#pragma unroll
+                for (int q = p + 1 - BO; q <= p; q++) {
+                    if (BO > 1 && p != RNP - 1) break;
+                    const int m = mb + r0 + RRPP * q;
+                    if (!FULL && m >= a.M) continue;
+                    float* dst = (float*)a.out + (size_t)m * a.ldo + n;
+                    if (RES)
+                        __builtin_nontemporal_store(o[q % BO], (f32x4*)dst);
+                    else
+                        *(f32x4*)dst = o[q % BO];
                 }
             }
         } else {  // 16-bit rows: 8 columns a lane
             const int c8 = 8 * (lane % HLPR), r0 = lane / HLPR;
             const int n = nw + c8;
+            float mx = 0.0f;
 #pragma unroll
-            for (int p = 0; p < 32 / HRPP; p++) {
+            for (int p = 0; p < HNP; p++) {
                 const int rr = r0 + HRPP * p, m = mb + rr;
                 if (!FULL && m >= a.M) continue;
                 f32x4 v0 = *(const f32x4*)(patch + rr * LD + c8) + cb0;
@@ -210,49 +247,82 @@ __device__ __forceinline__ void gemm_epilogue_body(const LtxGemmArgs& a, Fill fi
                     v0 = f32x4{gelu_tanh(v0[0]), gelu_tanh(v0[1]), gelu_tanh(v0[2]), gelu_tanh(v0[3])};
                     v1 = f32x4{gelu_tanh(v1[0]), gelu_tanh(v1[1]), gelu_tanh(v1[2]), gelu_tanh(v1[3])};
                 }
-                __builtin_nontemporal_store(u32x4{pack2<T>(v0[0], v0[1]), pack2<T>(v0[2], v0[3]),
-                                                  pack2<T>(v1[0], v1[1]), pack2<T>(v1[2], v1[3])},
-                                            (u32x4*)((uint16_t*)a.out + (size_t)m * ldo + n));
+                const u32x4 pk = {pack2<T>(v0[0], v0[1]), pack2<T>(v0[2], v0[3]), pack2<T>(v1[0], v1[1]),
+                                  pack2<T>(v1[2], v1[3])};
+                if (FULL) {
+                    ob[i % HOLD][p] = pk;
 #pragma unroll
-                for (int e = 0; e < 4; e++) bad += out_of_range<T>(v0[e]) + out_of_range<T>(v1[e]);
+                    for (int e = 0; e < 4; e++)
+                        mx = __builtin_elementwise_maximum(
+                            mx, __builtin_elementwise_maximum(__builtin_fabsf(v0[e]), __builtin_fabsf(v1[e])));
+                } else {
+                    __builtin_nontemporal_store(pk, (u32x4*)((uint16_t*)a.out + (size_t)m * ldo + n));
+#pragma unroll
+                    for (int e = 0; e < 4; e++) bad += out_of_range<T>(v0[e]) + out_of_range<T>(v1[e]);
+                }
+            }
+            if (FULL && !(mx <= RangeMax<T>::v))  // rare: count this block's values from the patch
+#pragma unroll
+                for (int p = 0; p < HNP; p++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        bad += out_of_range<T>(act(patch[(r0 + HRPP * p) * LD + c8 + e] + (e < 4 ? cb0[e] : cb1[e - 4])));
+        }
+        if (FULL && OUT != 1 && i % HOLD == HOLD - 1) {
+#pragma unroll
+            for (int h = 0; h < HOLD; h++) {
+                const int bb = mw + 32 * (i + 1 - HOLD + h);
+#pragma unroll
+                for (int p = 0; p < BNP; p++) {
+                    if (OUT == 2) {
+                        const int c = nw + 16 * p + (lane >> 2) - a.nsplit;
+                        __builtin_nontemporal_store(
+                            ob[h][p], (u32x4*)((uint16_t*)a.out2 + (size_t)c * a.M + bb + 8 * (lane & 3)));
+                    } else {
+                        const int m = bb + lane / HLPR + HRPP * p;
+                        __builtin_nontemporal_store(
+                            ob[h][p], (u32x4*)((uint16_t*)a.out + (size_t)m * ldo + nw + 8 * (lane % HLPR)));
+                    }
+                }
             }
         }
     }
     range_report(a.sat, bad);
 }
 
-template <typename T, int EPI, int NI, int NJ, int OUT, bool GELU, typename Fill>
+template <typename T, int EPI, int NI, int NJ, int OUT, bool GELU, int HOLD, typename Fill>
 __device__ __forceinline__ void gemm_epilogue_rows(const LtxGemmArgs& a, Fill fill, float* patch, int mw, int nw) {
     if (mw + 32 * NI <= a.M && (a.M & 7) == 0)
-        gemm_epilogue_body<T, EPI, NI, NJ, OUT, GELU, true>(a, fill, patch, mw, nw);
+        gemm_epilogue_body<T, EPI, NI, NJ, OUT, GELU, true, HOLD>(a, fill, patch, mw, nw);
     else
-        gemm_epilogue_body<T, EPI, NI, NJ, OUT, GELU, false>(a, fill, patch, mw, nw);
+        gemm_epilogue_body<T, EPI, NI, NJ, OUT, GELU, false, 1>(a, fill, patch, mw, nw);
 }
 
 // SF: the STORE epilogue's form fixed at compile time (bit 0 GELU, bit 1 f32
-// output), or -1 to take a.gelu and a.out_f32 at run time.
-template <typename T, int EPI, int NI, int NJ, typename Fill, int SF = -1>
+// output), or -1 to take a.gelu and a.out_f32 at run time. HOLD: the blocks
+// of 16-bit outputs held in registers before they are stored.
+template <typename T, int EPI, int NI, int NJ, typename Fill, int SF = -1, int HOLD = 1>
 __device__ __forceinline__ void gemm_epilogue_patch(const LtxGemmArgs& a, Fill fill, float* patch, int mw, int nw,
                                                     int n0) {
     if (EPI == LTX_EPI_STORE && SF >= 0) {
-        gemm_epilogue_rows<T, EPI, NI, NJ, (SF & 2) ? 1 : 0, (SF & 1) != 0>(a, fill, patch, mw, nw);
+        gemm_epilogue_rows<T, EPI, NI, NJ, (SF & 2) ? 1 : 0, (SF & 1) != 0, HOLD>(a, fill, patch, mw, nw);
     } else if (EPI == LTX_EPI_QKV) {
         if (n0 >= a.nsplit)
-            gemm_epilogue_rows<T, EPI, NI, NJ, 2, false>(a, fill, patch, mw, nw);
+            gemm_epilogue_rows<T, EPI, NI, NJ, 2, false, HOLD>(a, fill, patch, mw, nw);
         else
-            gemm_epilogue_rows<T, EPI, NI, NJ, 0, false>(a, fill, patch, mw, nw);
+            gemm_epilogue_rows<T, EPI, NI, NJ, 0, false, HOLD>(a, fill, patch, mw, nw);
     } else if (EPI == LTX_EPI_RESID_GATE) {
-        gemm_epilogue_rows<T, EPI, NI, NJ, 1, false>(a, fill, patch, mw, nw);
+        gemm_epilogue_rows<T, EPI, NI, NJ, 1, false, HOLD>(a, fill, patch, mw, nw);
     } else if (a.out_f32) {
         if (a.gelu)
-            gemm_epilogue_rows<T, EPI, NI, NJ, 1, true>(a, fill, patch, mw, nw);
+            gemm_epilogue_rows<T, EPI, NI, NJ, 1, true, HOLD>(a, fill, patch, mw, nw);
         else
-            gemm_epilogue_rows<T, EPI, NI, NJ, 1, false>(a, fill, patch, mw, nw);
+            gemm_epilogue_rows<T, EPI, NI, NJ, 1, false, HOLD>(a, fill, patch, mw, nw);
     } else {
         if (a.gelu)
-            gemm_epilogue_rows<T, EPI, NI, NJ, 0, true>(a, fill, patch, mw, nw);
+            gemm_epilogue_rows<T, EPI, NI, NJ, 0, true, HOLD>(a, fill, patch, mw, nw);
         else
-            gemm_epilogue_rows<T, EPI, NI, NJ, 0, false>(a, fill, patch, mw, nw);
+            gemm_epilogue_rows<T, EPI, NI, NJ, 0, false, HOLD>(a, fill, patch, mw, nw);
     }
 }
 

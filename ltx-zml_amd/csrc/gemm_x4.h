@@ -243,8 +243,8 @@ struct X4Gemm {
                         for (int r = 0; r < 4; r++)
                             p[(16 * e + 4 * (el >> 4) + r) * LD + 16 * j + (el & 15)] = acc[2 * b + e][j][r];
             };
-            gemm_epilogue_patch<T, EPI, 4, 4, decltype(fill), EPI == LTX_EPI_STORE ? SF : -1>(a, fill, (float*)patch,
-                                                                                              m0 + wm, n0 + wn, n0);
+            gemm_epilogue_patch<T, EPI, 4, 4, decltype(fill), EPI == LTX_EPI_STORE ? SF : -1, 4>(
+                a, fill, (float*)patch, m0 + wm, n0 + wn, n0);
             // every patch has been read back before the next tile's DMA
             meet();
         }
