@@ -217,7 +217,9 @@ int ltx_op_linear_q8(ltx_ctx* ctx, const void* a, const int8_t* q, const void* s
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): ltx_op_linear_q8 with the same arguments and results,
  * calling no hipMalloc / hipFree. Its scratch (the weights as bytes q + 128,
- * N * K bytes rounded up to 256, then the scale words, 4 N K / 128 bytes) is
+ * N * K bytes rounded up to 256, then the scale words, 4 N K / 128 bytes,
+ * and for the shapes ltx_op_linear_q8 runs on the four-wave GEMM, from 4,096
+ * rows, the weights dequantised to the operand type, 2 N K bytes) is
  * a static device array of LTX_NOALLOC_SCRATCH_BYTES on each GPU the library
  * runs on, held until the process ends; a shape needing more is refused with
  * an error. The kernels write all of the scratch they read on each call, so

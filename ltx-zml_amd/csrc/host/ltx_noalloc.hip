@@ -54,15 +54,23 @@ extern "C" int ltx_op_linear_q8_noalloc(ltx_ctx* c, const void* a, const int8_t*
         ltx::check_linear_q8(M, N, K, mode);
         ltx::LinearScratch sc{};
         if (ltx::linear_q8_needs_scratch(c, N, K, mode)) {
-            // weights as bytes q + 128, then the scale words, 256-byte aligned
-            const size_t nq = ((size_t)N * K + 255) & ~(size_t)255, np = (size_t)N * (K / LTX_GROUP) * 4;
-            if (nq + np > LTX_NOALLOC_SCRATCH_BYTES)
-                throw ltx::Error("ltx_op_linear_q8_noalloc: N * K + 4 N K / 128 bytes exceed the " +
-                                 std::to_string(LTX_NOALLOC_SCRATCH_BYTES) + "-byte scratch");
+            // weights as bytes q + 128, then the scale words, then (where
+            // ltx_op_linear_q8 runs the four-wave kernel) the weights
+            // dequantised to the operand type, each 256-byte aligned
+            auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+            const size_t nq = al((size_t)N * K), np = al((size_t)N * (K / LTX_GROUP) * 4);
+            const size_t nw = ltx::x4_shape(c, mode, M, N, K, K) ? (size_t)N * K * 2 : 0;
+            if (nq + np + nw > LTX_NOALLOC_SCRATCH_BYTES)
+                throw ltx::Error(std::string("ltx_op_linear_q8_noalloc: ") +
+                                 (nw ? "N * K + 4 N K / 128 + 2 N K bytes (the 16-bit weight copy of the "
+                                       "four-wave GEMM, from 4,096 rows)"
+                                     : "N * K + 4 N K / 128 bytes") +
+                                 " exceed the " + std::to_string(LTX_NOALLOC_SCRATCH_BYTES) + "-byte scratch");
             char* base = (char*)ltx::noalloc_scratch(c->device);
             if (!base) throw ltx::Error("ltx_op_linear_q8_noalloc: scratch not set up on this device");
             sc.q = (uint32_t*)base;
             sc.pairs = (uint32_t*)(base + nq);
+            sc.w16 = nw ? base + nq + np : nullptr;
         }
         HIPC(hipSetDevice(c->device));
         ltx::linear_q8(c, a, q, scales, scale_f16, bias, y, out_f32, M, N, K, gelu, mode, sc, (hipStream_t)stream);

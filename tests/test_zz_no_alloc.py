@@ -3,8 +3,9 @@
 The no-alloc entry point runs the same kernels with its scratch in the
 library's static device array, so its output must equal the allocating entry
 point's bit for bit. Two calls in a row, the second with a smaller input (so a
-stale first-call scratch would show), in both 16-bit modes with f16 and f32
-scales; the F32 mode (no scratch); and a shape whose scratch exceeds the
+stale first-call scratch would show), from a shape on the four-wave GEMM
+(weights dequantised into the scratch) down to ones on the W8A16 kernel, in
+both 16-bit modes with f16 and f32 scales; the F32 mode (no scratch); and a shape whose scratch exceeds the
 array is refused.
 """
 import numpy as np
@@ -46,7 +47,10 @@ def _both(ctx, mode, M, N, K, seed, scale_f16, gelu, out_f32):
 @pytest.mark.parametrize("scale_f16", [1, 0])
 @pytest.mark.parametrize("mode", [rt.MODE_F16, rt.MODE_BF16])
 def test_noalloc_equals_linear_q8(ctx, mode, scale_f16):
-    for M, N, K, gelu, out_f32 in ((1000, 4096, 4096, True, False), (300, 512, 1024, False, True)):
+    # 4,100 rows: the four-wave GEMM on the weights dequantised into the
+    # scratch (ragged last row tile); then smaller calls on the W8A16 kernel
+    for M, N, K, gelu, out_f32 in ((4100, 4096, 4096, False, False), (1000, 4096, 4096, True, False),
+                                   (300, 512, 1024, False, True)):
         say(f"linear_q8_noalloc mode={mode} scale_f16={scale_f16} M={M} N={N} K={K}")
         y0, y1 = _both(ctx, mode, M, N, K, M + N + K + scale_f16, scale_f16, gelu, out_f32)
         assert torch.isfinite(y0).all().item()
@@ -76,8 +80,9 @@ def test_noalloc_without_scratch_paths(ctx):
 
 
 def test_noalloc_refuses_oversized_scratch(ctx):
-    """N K + 4 N K / 128 beyond the static array: refused with an error
-    before any launch (the inputs are never read)."""
+    """N K + 4 N K / 128 (plus 2 N K from 4,096 rows) beyond the static
+    array: refused with an error before any launch (the inputs are never
+    read)."""
     say("linear_q8_noalloc oversized shape is refused")
     M, N, K = 256, 32768, 4096  # 128 MiB of weights > the 66 MiB array
     a = torch.empty((M, K), dtype=torch.float16, device="cuda")
@@ -85,4 +90,14 @@ def test_noalloc_refuses_oversized_scratch(ctx):
     s = torch.empty((N, K // 128), dtype=torch.float16, device="cuda")
     y = torch.empty((M, N), dtype=torch.float16, device="cuda")
     with pytest.raises(rt.LtxError, match="exceed"):
+        ctx.linear_q8(a, q, s, None, y, mode=rt.MODE_F16, noalloc=True)
+    # from 4,096 rows the 16-bit weight copy (2 N K) counts too: 32 MiB of
+    # weights fit without it (33 MiB) but not with it (97 MiB)
+    M, N, K = 4096, 8192, 4096
+    say(f"linear_q8_noalloc M={M} N={N} K={K}: no room for the 16-bit weight copy, refused")
+    a = torch.empty((M, K), dtype=torch.float16, device="cuda")
+    q = torch.empty((N, K), dtype=torch.int8, device="cuda")
+    s = torch.empty((N, K // 128), dtype=torch.float16, device="cuda")
+    y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    with pytest.raises(rt.LtxError, match="2 N K bytes"):
         ctx.linear_q8(a, q, s, None, y, mode=rt.MODE_F16, noalloc=True)
