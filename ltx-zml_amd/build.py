@@ -27,7 +27,7 @@ LIB = PKG / "libltx_amd.so"
 CEILING = PKG / "mfma_ceiling"
 INCLUDE = PKG.parent / "include"
 ROCM = pathlib.Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
-KERNELS = ["k_gemm", "k_attn", "k_norm", "k_f32", "k_core"]
+KERNELS = ["k_gemm", "k_gemm_s4", "k_attn", "k_norm", "k_f32", "k_core"]
 HOST = ["ltx_runtime", "ltx_forward", "ltx_weights", "ltx_rope", "ltx_loader", "ltx_core", "sha256"]
 
 HIPCC_FLAGS = [

@@ -41,8 +41,8 @@ static const int kX4Shapes[6][2] = {{3 * LTX_D, LTX_D}, {LTX_D, LTX_D}, {LTX_D, 
 // Split-K slices of a GEMM whose 256 x tn output tiles would fill at most
 // half the CUs: the largest power of two S <= 8 with tiles * S <= CUs and
 // K / S a multiple of 128 of at least 512 (eight K-tiles per slice).
-static int gemm_ksplit(int num_cu, int M, int N, int K, int tn = 256) {
-    const int tiles = ((M + 255) / 256) * (N / tn);
+static int gemm_ksplit(int num_cu, int M, int N, int K, int tn = 256, int tm = 256) {
+    const int tiles = ((M + tm - 1) / tm) * (N / tn);
     int s = 1;
     while (s < 8 && tiles * s * 2 <= num_cu && K % (256 * s) == 0 && K / (s * 2) >= 512) s *= 2;
     return s;
@@ -56,6 +56,21 @@ bool x4_shape(const ltx_ctx* c, int mode, int M, int N, int K, int lda) {
     if (c->gemm_x4 == 2) return true;
     // where its 256 x 256 tiles fill the CUs: the sizes that need no split-K
     return M >= 4096 && gemm_ksplit(c->num_cu, M, N, K) == 1;
+}
+
+bool s4_shape(const ltx_ctx* c, int mode, int M, int N, int K, int lda, bool q8) {
+    if (mode != LTX_MODE_F16 && mode != LTX_MODE_BF16) return false;
+    if (!c->gemm_s4 || !c->gemm_dma) return false;
+    if (M <= 0 || N % 128 || K % 128 || lda < K || lda % 8) return false;
+    if ((uint64_t)M * lda * 2 >= (1ull << 31) || (uint64_t)N * K * (q8 ? 1 : 2) >= (1ull << 31)) return false;
+    if (c->gemm_s4 == 2) return true;
+    // int8 weights where the 256 x 256 kernels would split K (their tiles
+    // fill at most half the CUs) over at most 4,096: there it needs no
+    // split-K reduce (the context k|v projection, the 4096-wide projections
+    // below 4,096 rows). With 16-bit weights, or K = 16,384, its 128 x 128
+    // tiles (half the flops per byte moved) measured slower than the split
+    // 256 x 256 kernels; with no split (q|k|v at 1,024 rows) slower too.
+    return q8 && M < 4096 && K <= 4096 && gemm_ksplit(c->num_cu, M, N, K) > 1;
 }
 
 static void carve16(Carve& c, Ws16& w, size_t T, size_t S, const ltx_ctx* ctx, int mode) {
@@ -208,6 +223,29 @@ static void gemm16(ltx_ctx* c, int mode, const LtxProj& p, const void* A, int M,
                           epi == LTX_EPI_STORE && g.out_f32 ? "32" : "", epi == LTX_EPI_STORE && g.gelu ? "_gelu" : "");
             const int nitems = g.tiles_m * g.tiles_n;
             c->launch(name, c->gemm_persistent ? std::min(nitems, c->num_cu) : nitems, 1, 1, 256, &g, st, label);
+            return;
+        }
+    }
+    // Small grids: 128 x 128 tiles, two workgroups a CU, int8 weights laid
+    // out for the LDS-DMA kernels (bytes q + 128, scale words) or 16-bit
+    // weights; split K only while even those tiles fill at most half the CUs
+    {
+        const void* wb = p.q8 ? (p.qflip && p.s2.p ? p.q.p : nullptr) : (mode == LTX_MODE_BF16 ? p.w_bf16.p : p.w_f16.p);
+        if (wb && s4_shape(c, mode, M, p.N, p.K, lda, p.q8) && g.ldo % 8 == 0 && al16(A) && al16(wb) && al16(g.out) &&
+            al16(g.out2) && al16(g.resid) && al16(g.bias) && al16(g.ada.tstab) && al16(g.ada.sst)) {
+            g.b = wb;
+            g.scales = p.q8 ? p.s2.p : nullptr;
+            g.tiles_m = (M + 127) / 128;
+            g.tiles_n = p.N / 128;
+            g.ksplit = g.part ? gemm_ksplit(c->num_cu, M, p.N, p.K, 128, 128) : 1;
+            std::snprintf(name, sizeof(name), "ltx_gemm_s4_%s_%s_%s", msuffix(mode),
+                          p.q8 ? (p.scale_f16 ? "i8f16" : "i8f32") : "w16", es);
+            const int nitems = g.tiles_m * g.tiles_n * g.ksplit;
+            c->launch(name, c->gemm_persistent ? std::min(nitems, 2 * c->num_cu) : nitems, 1, 1, 256, &g, st, label);
+            if (g.ksplit > 1) {
+                std::snprintf(name, sizeof(name), "ltx_gemm_reduce_%s_%s", msuffix(mode), es);
+                c->launch(name, p.N / 64, (M + 63) / 64, 1, 256, &g, st, "splitk_reduce");
+            }
             return;
         }
     }

@@ -92,6 +92,10 @@ struct ltx_ctx {
     // 0 never, 1 where its tiles fill the CUs (M >= 4,096 and no split-K),
     // 2 wherever the shape allows (tests)
     int gemm_x4 = 1;
+    // the small-grid GEMM (128 x 128 tiles): 0 never, 1 for int8 weights
+    // where the 256 x 256 kernels would split K over at most 4,096 (M below
+    // 4,096), 2 wherever the shape allows (tests)
+    int gemm_s4 = 1;
     int num_cu = 256;             // compute units: the persistent GEMM's grid bound
     bool gemm_persistent = true;  // LDS-DMA GEMM: at most one workgroup per CU, looping over tiles
     bool attn_pp = true;
@@ -165,6 +169,8 @@ struct LinearScratch {
 // Whether the four-wave 16-bit GEMM takes an M x N x K product with A rows of
 // lda elements (shape, 32-bit buffer offsets and the context's setting).
 bool x4_shape(const ltx_ctx* c, int mode, int M, int N, int K, int lda);
+// Whether the small-grid GEMM takes it (q8: int8 weights, else 16-bit).
+bool s4_shape(const ltx_ctx* c, int mode, int M, int N, int K, int lda, bool q8);
 // Shape and mode checks of the isolated int8 GEMM (throws Error), made before
 // any scratch is sized from N and K.
 void check_linear_q8(int M, int N, int K, int mode);

@@ -9,7 +9,8 @@
 
 // gfx950 code objects, embedded at build time (ltx_codeobjects.S).
 extern "C" {
-extern const unsigned char ltx_co_k_gemm[], ltx_co_k_attn[], ltx_co_k_norm[], ltx_co_k_f32[], ltx_co_k_core[];
+extern const unsigned char ltx_co_k_gemm[], ltx_co_k_gemm_s4[], ltx_co_k_attn[], ltx_co_k_norm[], ltx_co_k_f32[],
+    ltx_co_k_core[];
 }
 
 namespace ltx {
@@ -179,13 +180,16 @@ int ltx_init(int device, ltx_ctx** out) {
         // LTX_GEMM_GRID=tile: one workgroup per output tile instead of the
         // persistent grid of one per CU; LTX_GEMM_Q8=reg: the register-staged
         // int8 GEMM everywhere; LTX_GEMM_X4=off / all: the four-wave 16-bit
-        // GEMM nowhere / wherever the shape allows; LTX_ATTN_VARIANT=w8: the any-length attention
+        // GEMM nowhere / wherever the shape allows; LTX_GEMM_S4=off / all: the
+        // small-grid GEMM likewise; LTX_ATTN_VARIANT=w8: the any-length attention
         // everywhere, =pp: the streaming ping-pong attention also for 64-256
         // keys (the kernels each test exercises beside the defaults)
         if (const char* e = std::getenv("LTX_GEMM_GRID")) c->gemm_persistent = std::strcmp(e, "tile") != 0;
         if (const char* e = std::getenv("LTX_GEMM_Q8")) c->gemm_dma = std::strcmp(e, "reg") != 0;
         if (const char* e = std::getenv("LTX_GEMM_X4"))
             c->gemm_x4 = std::strcmp(e, "off") == 0 ? 0 : std::strcmp(e, "all") == 0 ? 2 : 1;
+        if (const char* e = std::getenv("LTX_GEMM_S4"))
+            c->gemm_s4 = std::strcmp(e, "off") == 0 ? 0 : std::strcmp(e, "all") == 0 ? 2 : 1;
         if (const char* e = std::getenv("LTX_ATTN_VARIANT")) {
             c->attn_pp = std::strcmp(e, "w8") != 0;
             c->attn_kv = c->attn_pp && std::strcmp(e, "pp") != 0;
@@ -193,7 +197,8 @@ int ltx_init(int device, ltx_ctx** out) {
         HIPC(hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking));  // default priority
         for (auto& e : c->side_ev) HIPC(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         for (auto& e : c->marks) HIPC(hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventDisableSystemFence));
-        for (const unsigned char* co : {ltx_co_k_gemm, ltx_co_k_attn, ltx_co_k_norm, ltx_co_k_f32, ltx_co_k_core}) {
+        for (const unsigned char* co :
+             {ltx_co_k_gemm, ltx_co_k_gemm_s4, ltx_co_k_attn, ltx_co_k_norm, ltx_co_k_f32, ltx_co_k_core}) {
             hipModule_t m;
             HIPC(hipModuleLoadData(&m, co));
             c->modules.push_back(m);

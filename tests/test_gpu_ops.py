@@ -178,15 +178,19 @@ def test_linear_q8_onehot_extreme_f32_scales(ctx, mode, exp_range):
         assert ((want != 0) & (np.abs(want) < 6.1e-5)).sum() > 1000  # subnormal operands were exercised
 
 
-VARIANT_ENV = {"reg": ("LTX_GEMM_Q8", "reg"), "x4": ("LTX_GEMM_X4", "all")}
+VARIANT_ENV = {"reg": ("LTX_GEMM_Q8", "reg"), "x4": ("LTX_GEMM_X4", "all"), "s4off": ("LTX_GEMM_S4", "off"),
+               "s4all": ("LTX_GEMM_S4", "all")}
 
 
-@pytest.mark.parametrize("variant", ["reg", "x4"])
+@pytest.mark.parametrize("variant", ["reg", "x4", "s4off", "s4all"])
 def test_linear_q8_variants(monkeypatch, variant):
     """Other GEMM kernels forced everywhere, in a context of their own:
     - reg: the register-staged int8 GEMM (the fallback of the LDS-DMA one);
     - x4: the four-wave 16-bit GEMM after the per-call dequantisation
-      (ltx_gemm_dq16_*), which the block uses from 4,096 rows.
+      (ltx_gemm_dq16_*), which the block uses from 4,096 rows;
+    - s4off: no small-grid kernel, so these shapes (below 4,096 rows, most
+      of which take it by default) run the 256 x 256 LDS-DMA int8 kernel;
+    - s4all: the small-grid kernel (128 x 128 tiles) at every shape.
     The one-hot exactness check (every output one weight operand, bit for
     bit: the dequantised operands, f16 and f32 scales, both operand types),
     then GEMMs against the oracle: ragged M with a bias, and for x4 also GELU

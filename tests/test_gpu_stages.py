@@ -157,35 +157,50 @@ def test_unquantised_block_stages(ctx, block0_w16, mode, T, S):
         assert r["y"] <= 2e-3
 
 
-@pytest.fixture(scope="module")
-def ctx_x4():
-    """A context whose 16-bit GEMMs all take the four-wave kernel
-    (LTX_GEMM_X4=all; by default it runs from 4,096 rows), so that these small
-    T exercise it: the int8 projections dequantised per forward by
-    ltx_gemm_dq16_*, a ragged last row tile, and every epilogue (QKV split
-    with V^T, gated residual, GELU, 16-bit stores)."""
+GEMM_VARIANTS = {
+    # every 16-bit GEMM on the four-wave kernel (by default it runs from 4,096
+    # rows): the int8 projections dequantised per forward by ltx_gemm_dq16_*,
+    # a ragged last row tile, and every epilogue (QKV split with V^T, gated
+    # residual, GELU, 16-bit stores)
+    "x4": ("LTX_GEMM_X4", "all"),
+    # no small-grid kernel: at these sizes the 256 x 256 LDS-DMA kernels with
+    # K split over workgroups and the reduce launch
+    "s4off": ("LTX_GEMM_S4", "off"),
+    # the small-grid kernel (128 x 128 tiles) for every projection, the
+    # unquantised ones included, split over K where even its tiles fill at
+    # most half the CUs
+    "s4all": ("LTX_GEMM_S4", "all"),
+}
+
+
+@pytest.fixture(scope="module", params=sorted(GEMM_VARIANTS))
+def ctx_gemm(request):
+    """A context with one GEMM path forced by its environment setting (read
+    when the context is made)."""
     import os
-    old = os.environ.get("LTX_GEMM_X4")
-    os.environ["LTX_GEMM_X4"] = "all"
+    var, val = GEMM_VARIANTS[request.param]
+    old = os.environ.get(var)
+    os.environ[var] = val
     try:
         c = rt.Context(0)
     finally:
         if old is None:
-            del os.environ["LTX_GEMM_X4"]
+            del os.environ[var]
         else:
-            os.environ["LTX_GEMM_X4"] = old
-    yield c
+            os.environ[var] = old
+    yield request.param, c
     c.close()
 
 
 @pytest.mark.parametrize("weights", ["int8", "bf16"])
 @pytest.mark.parametrize("T,S", [(256, 64), (250, 40)])
 @pytest.mark.parametrize("mode", ["f16", "bf16"])
-def test_block_stages_x4(ctx_x4, block0, block0_w16, mode, T, S, weights):
-    """The block with every projection on the four-wave 16-bit GEMM: int8
-    weights (dequantised for the forward) and the unquantised block, every
-    stage against the oracle under the gates of test_block_stages."""
-    say(f"block stages four-wave GEMM mode={mode} T={T} S={S} weights={weights}")
+def test_block_stages_gemm_variants(ctx_gemm, block0, block0_w16, mode, T, S, weights):
+    """The block with its projections on another GEMM path: int8 weights and
+    the unquantised block, every stage against the oracle under the gates of
+    test_block_stages."""
+    variant, c = ctx_gemm
+    say(f"block stages gemm={variant} mode={mode} T={T} S={S} weights={weights}")
     bt = block0 if weights == "int8" else block0_w16
     inp = synth.make_inputs(T, S, sigma=0.7)
     cos, sin = rt.rope_tables(inp["grid"])
@@ -193,9 +208,9 @@ def test_block_stages_x4(ctx_x4, block0, block0_w16, mode, T, S, weights):
     if key not in _CACHE:
         _CACHE[key] = oracle.block_forward(bt, inp, cos, sin, chunk=16 if T % 16 == 0 else 0, stages=True)
     want, wst = _CACHE[key]
-    w = ctx_x4.upload(bt)
-    y = forward(ctx_x4, w, inp, cos, sin, mode)
-    g = gpu_stages(ctx_x4, mode, T, S)
+    w = c.upload(bt)
+    y = forward(c, w, inp, cos, sin, mode)
+    g = gpu_stages(c, mode, T, S)
     w.free()
     r = compare_stages(g, y, want, wst, inp["x"].astype(np.float64))
     say("  " + " ".join(f"{k}={v:.2e}" for k, v in r.items()))
