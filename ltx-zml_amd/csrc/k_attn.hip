@@ -313,17 +313,17 @@ __device__ __forceinline__ float asp_quad_max(float x) {
 //
 // LDS: K tiles of 64 rows x 256 B, 16-byte chunk c of row r in slot
 // c ^ (r & 15); V^T tiles of 128 rows x 128 B with chunk c of row d in slot
-// c ^ ((d >> 1) & 7). Three stages each, distinct objects.
+// c ^ ((d >> 1) & 7). Four stages each (streaming form), distinct objects.
 //
 // DMA and waits (G0 = waves 0-3 lead, G1 = waves 4-7 follow one phase
-// later): G0 issues all of K(t+2) and V(t+1) (its slices and G1's) at the
-// start of its softmax phase t, two phases before its MFMA phase t+2 reads
-// them, and at the end of softmax phase t waits for what it issued one
-// softmax phase earlier: K(t+1) and V(t) are complete before the barrier
-// after which G0's MFMA phase t+1 (and, half a step later, G1's) reads
-// them. G1 issues no DMA: its softmax phase runs one phase after G0's, so
-// slices it issued would have only one phase to land (measured 1 % slower
-// on the whole kernel).
+// later): G0 issues all of K(t+2) and V(t+2) (its slices and G1's) at the
+// start of its softmax phase t, and at the end of softmax phase t waits for
+// what it issued one softmax phase earlier: K(t+1) and V(t+1) are complete
+// before the barrier after which G0's MFMA phase t+1 (and, half a step
+// later, G1's) reads K(t+1); V(t+1) is read from the softmax phase t+1 on
+// (the first fragments of PV(t+1)). G1 issues no DMA: its softmax phase runs
+// one phase after G0's, so slices it issued would have only one phase to
+// land (measured 1 % slower on the whole kernel).
 //
 // The softmax state (running max m, partial sums l) is held in vector
 // values: as arrays in the kernel's state the compiler placed them in LDS,
@@ -331,17 +331,19 @@ __device__ __forceinline__ float asp_quad_max(float x) {
 __shared__ __attribute__((aligned(1024))) uint8_t app_k0[16384];
 __shared__ __attribute__((aligned(1024))) uint8_t app_k1[16384];
 __shared__ __attribute__((aligned(1024))) uint8_t app_k2[16384];
+__shared__ __attribute__((aligned(1024))) uint8_t app_k3[16384];
 __shared__ __attribute__((aligned(1024))) uint8_t app_v0[16384];
 __shared__ __attribute__((aligned(1024))) uint8_t app_v1[16384];
 __shared__ __attribute__((aligned(1024))) uint8_t app_v2[16384];
+__shared__ __attribute__((aligned(1024))) uint8_t app_v3[16384];
 
 template <int S>
 __device__ __forceinline__ uint8_t* app_k() {
-    return S == 0 ? app_k0 : S == 1 ? app_k1 : app_k2;
+    return S == 0 ? app_k0 : S == 1 ? app_k1 : S == 2 ? app_k2 : app_k3;
 }
 template <int S>
 __device__ __forceinline__ uint8_t* app_v() {
-    return S == 0 ? app_v0 : S == 1 ? app_v1 : app_v2;
+    return S == 0 ? app_v0 : S == 1 ? app_v1 : S == 2 ? app_v2 : app_v3;
 }
 
 
@@ -515,37 +517,41 @@ struct AttnPP {
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // MFMA phase t then softmax phase t (T3 = t mod 3); returns after the
+    // MFMA phase t then softmax phase t (T4 = t mod 4); returns after the
     // softmax phase's barrier (or after the MFMA phase's when t == nt).
     // FULL: 1 <= t and t + 2 < nt, every operation present. The wave in its
     // MFMA phase takes issue priority over the other wave of its SIMD.
-    template <int T3, bool FULL>
+    //
+    // K and V^T both run two tiles ahead in four stages each: the softmax
+    // phase t issues K(t + 2) and V(t + 2) and waits for K(t + 1) and V(t + 1),
+    // so V(t) is complete one phase before the PV(t) that reads it, and the
+    // softmax phase reads PV(t)'s first four V^T fragments (prefetch_v): the
+    // MFMA phase opens with MFMAs instead of waiting out those reads. (With V one tile ahead in three stages, V(t) completed
+    // only at the barrier before PV(t).)
+    template <int T4, bool FULL>
     __device__ __forceinline__ void step(int t) {
         __builtin_amdgcn_s_setprio(1);
-        mfma_phase(app_k<T3>(), app_v<(T3 + 2) % 3>(), FULL || t < nt, FULL || t >= 1);
+        mfma_phase<true>(app_k<T4>(), app_v<(T4 + 3) % 4>(), FULL || t < nt, FULL || t >= 1);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
         barrier();
         if (!FULL && t >= nt) return;
-        const bool dk = FULL || t + 2 < nt, dv = FULL || t + 1 < nt;
-        if (g == 0) {
-            if (dk) dma_k<(T3 + 2) % 3>(t + 2);
-            if (dv) dma_v<(T3 + 1) % 3>(t + 1);
+        // read first, before this phase's DMA is in flight (the compiler's
+        // LDS-DMA tracking made reads behind it wait for it)
+        prefetch_v(app_v<T4>());
+        __builtin_amdgcn_sched_barrier(0);
+        const bool dkv = FULL || t + 2 < nt;
+        if (g == 0 && dkv) {
+            dma_k<(T4 + 2) % 4>(t + 2);
+            dma_v<(T4 + 2) % 4>(t + 2);
         }
         __builtin_amdgcn_sched_barrier(0);
         softmax(!FULL && t == 0);
-#pragma unroll
-        for (int kc = 0; kc < 2; kc++)
-#pragma unroll
-            for (int qb = 0; qb < 2; qb++) asm volatile("" ::"v"(__builtin_bit_cast(u32x4, pf[kc][qb])));
-        asm volatile("" ::"v"(l), "v"(m));
-        asm volatile("" ::"v"(sb[0]), "v"(sb[1]));
+        pin_softmax_pre();
         __builtin_amdgcn_sched_barrier(0);
         if (g == 0) {
-            if (dk && dv)
+            if (dkv)
                 __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(8));
-            else if (dk || dv)
-                __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(4));
             else
                 __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(0));
         }
@@ -671,25 +677,28 @@ struct AttnPP {
         setup(h, w, lane);
         load_q(qf, h, q0, lane);
         reset();
-        if (g == 0) {
+        if (g == 0) {  // K(0) and V(0) complete, K(1) and V(1) in flight
             dma_k<0>(0);
-            dma_k<1>(1);
             dma_v<0>(0);
+            dma_k<1>(1);
+            dma_v<1>(1);
             __builtin_amdgcn_s_waitcnt(ASP_WAIT_VM(8));
         }
         __builtin_amdgcn_s_barrier();
         if (g == 1) __builtin_amdgcn_s_barrier();
         step<0, false>(0);
         int u = 1;
-        for (; u + 4 < nt; u += 3) {
+        for (; u + 5 < nt; u += 4) {
             step<1, true>(u);
             step<2, true>(u + 1);
-            step<0, true>(u + 2);
+            step<3, true>(u + 2);
+            step<0, true>(u + 3);
         }
-        for (; u <= nt; u += 3) {
+        for (; u <= nt; u += 4) {
             step<1, false>(u);
             if (u + 1 <= nt) step<2, false>(u + 1);
-            if (u + 2 <= nt) step<0, false>(u + 2);
+            if (u + 2 <= nt) step<3, false>(u + 2);
+            if (u + 3 <= nt) step<0, false>(u + 3);
         }
         if (g == 0) __builtin_amdgcn_s_barrier();
         // every wave has passed its last barrier: the K stages hold the
