@@ -29,7 +29,7 @@ struct Carve {
 
 struct Ws16 {
     void *n_msa, *qk16, *vt1, *qh1, *kh1, *glog1, *o1, *x_sa, *attn_in, *q2_16, *glog2, *enc, *k2_16, *vt2, *qh2,
-        *kh2, *o2, *x_ca, *ff_in, *h, *part;
+        *kh2, *o2, *x_ca, *ff_in, *h, *part, *part2;
     void* dq[6];  // 16-bit weights of qkv1, o1, q2, o2, ff1, ff2 for the four-wave GEMM (NULL: not used)
 };
 
@@ -73,6 +73,12 @@ bool s4_shape(const ltx_ctx* c, int mode, int M, int N, int K, int lda, bool q8)
     return q8 && M < 4096 && K <= 4096 && gemm_ksplit(c->num_cu, M, N, K) > 1;
 }
 
+// The small-T schedule of the block forward (side stream from the first
+// RMSNorm + modulate on).
+static bool side_early(const ltx_ctx* c, size_t T) {
+    return c->side_early == 2 || (c->side_early == 1 && T < (size_t)kEarlySideRows);
+}
+
 static void carve16(Carve& c, Ws16& w, size_t T, size_t S, const ltx_ctx* ctx, int mode) {
     const size_t D = LTX_D;
     const int num_cu = ctx->num_cu;
@@ -106,6 +112,13 @@ static void carve16(Carve& c, Ws16& w, size_t T, size_t S, const ltx_ctx* ctx, i
         if (k > 1) part = std::max(part, (size_t)k * sh[0] * sh[1] * 4);
     }
     w.part = part ? c.take(part) : nullptr;
+    // the context k|v GEMM's own partial sums when it runs on the side
+    // stream beside the main chain's split GEMMs
+    w.part2 = nullptr;
+    if (side_early(ctx, T)) {
+        const int k = gemm_ksplit(num_cu, (int)S, 2 * LTX_D, LTX_D);
+        if (k > 1) w.part2 = c.take((size_t)k * S * 2 * LTX_D * 4);
+    }
     for (int i = 0; i < 6; i++) {
         const int N = kX4Shapes[i][0], K = kX4Shapes[i][1];
         w.dq[i] = x4_shape(ctx, mode, (int)T, N, K, K) ? c.take((size_t)N * K * 2) : nullptr;
@@ -529,6 +542,45 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     // self-attention: n = modulate(rms(x), ada1, ada0); fused q|k|v GEMM
     norm_mod(c, mode, x, b.n_msa, ada, T, 0, 1, st,
              mode == LTX_MODE_F16 ? (const unsigned long long*)w->f16_over.p : nullptr);
+    hipStream_t sd = c->side;
+    auto fail_check = [&]() {
+        if (fail_in_capture()) {
+            hipStreamCaptureStatus cst = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(st, &cst) == hipSuccess && cst == hipStreamCaptureStatusActive)
+                throw Error("injected failure inside a graph capture, after the second stream joined it [LTX_FAIL_CAPTURE]");
+        }
+    };
+    // The context side of the cross-attention: K/V modulation, fused k|v
+    // GEMM (split-K partial sums in `part`), on stream s.
+    auto ctx_side = [&](hipStream_t s, void* part) {
+        LtxEncArgs ea{ctxv, (const float*)w->psst.p, pts2, b.enc, S, sat};
+        c->launch(mode == LTX_MODE_BF16 ? "ltx_enc_bf16" : "ltx_enc_f16", S, 1, 1, 256, &ea, s);
+        LtxGemmArgs gk{};
+        gk.out = b.k2_16;
+        gk.out2 = b.vt2;
+        gk.nsplit = LTX_D;
+        gk.sat = sat;
+        gk.part = (float*)part;
+        gemm16(c, mode, w->kv2, b.enc, S, LTX_D, LTX_EPI_QKV, gk, s, "gemm:kv2");
+    };
+    // Small T (early): the 256-row GEMM tiles and attention query tiles
+    // leave CUs idle, and the side stream fills them from here on: the
+    // self-attention gate logits beside the q|k|v GEMM, then the whole
+    // context side (K/V modulation, k|v GEMM with its own partial sums, k
+    // norm) beside the self-attention branch; later the cross-attention
+    // gate logits beside the q2 GEMM. Large T: side work starts only after
+    // the persistent GEMMs, whose one-workgroup-per-CU grids it would
+    // otherwise hold back, and ends before the attentions, which it would
+    // slow as much as it gains.
+    const bool early = side_early(c, (size_t)T);
+    if (early) {
+        stream_after(sd, st, c->side_ev[0]);
+        fail_check();
+        gate16(c, mode, w->g1, b.n_msa, T, (float*)b.glog1, sd);
+        HIPC(hipEventRecord(c->side_ev[1], sd));  // glog1 ready
+        ctx_side(sd, b.part2);
+        qknorm16(c, mode, b.k2_16, LTX_D, w->kn2.p, nullptr, nullptr, b.kh2, S, 1.0f, sd);
+    }
     LtxGemmArgs g{};
     g.out = b.qk16;
     g.out2 = b.vt1;
@@ -536,25 +588,20 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     g.sat = sat;
     g.part = (float*)b.part;  // split-K partial sums (small grids)
     gemm16(c, mode, w->qkv1, b.n_msa, T, LTX_D, LTX_EPI_QKV, g, st, "gemm:qkv1", dq[0]);
-    // The self-attention gate logits on the side stream, beside the q/k
-    // norms (both read only what the GEMMs above wrote). Side work starts
-    // after the persistent GEMM before it, whose one-workgroup-per-CU grid it
-    // would otherwise hold back, and ends before the attention, which it
-    // would slow as much as it gains.
-    hipStream_t sd = c->side;
-    stream_after(sd, st, c->side_ev[0]);
-    if (fail_in_capture()) {
-        hipStreamCaptureStatus cst = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(st, &cst) == hipSuccess && cst == hipStreamCaptureStatusActive)
-            throw Error("injected failure inside a graph capture, after the second stream joined it [LTX_FAIL_CAPTURE]");
+    if (!early) {
+        // the self-attention gate logits beside the q/k norms (both read
+        // only what the GEMMs above wrote)
+        stream_after(sd, st, c->side_ev[0]);
+        fail_check();
+        gate16(c, mode, w->g1, b.n_msa, T, (float*)b.glog1, sd);
+        HIPC(hipEventRecord(c->side_ev[1], sd));  // glog1 ready
     }
-    gate16(c, mode, w->g1, b.n_msa, T, (float*)b.glog1, sd);
     {  // q and k norms + RoPE in one pass (the RoPE rows read once)
         LtxQkNorm2Args qa{b.qk16, (const float*)w->qn1.p, (const float*)w->kn1.p, cs, sn, b.qh1, b.kh1,
                           T, 2 * LTX_D, kAttnC, 1.0f, sat};
         c->launch(mode == LTX_MODE_BF16 ? "ltx_qknorm2_bf16" : "ltx_qknorm2_f16", T, 1, 1, 256, &qa, st);
     }
-    stream_after(st, sd, c->side_ev[1]);
+    HIPC(hipStreamWaitEvent(st, c->side_ev[1], 0));
     attn16(c, mode, b.qh1, b.kh1, b.vt1, (const float*)b.glog1, b.o1, T, T, true, st, "attn:self", sat, true);
     g = LtxGemmArgs{};
     g.out = b.x_sa;
@@ -566,6 +613,10 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
     gemm16(c, mode, w->o1, b.o1, T, LTX_D, LTX_EPI_RESID_GATE, g, st, "gemm:o1", dq[1]);
     // cross-attention
     norm_mod(c, mode, (const float*)b.x_sa, b.attn_in, ada, T, 6, 7, st);
+    if (early) {
+        stream_after(sd, st, c->side_ev[2]);
+        gate16(c, mode, w->g2, b.attn_in, T, (float*)b.glog2, sd);
+    }
     g = LtxGemmArgs{};
     g.out = b.q2_16;
     g.ldo = LTX_D;
@@ -578,22 +629,18 @@ void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const
         // GEMM's split-K reduce beside them interleaved so badly that they
         // took 0.57 and 0.39 ms instead of 0.09 and 0.01 (28,672 tokens).
         MarkScope marks(c, T >= kMarkRows);
-        // the cross-attention gate logits on the side stream, beside the
-        // context side (K/V modulation, k|v GEMM) and the q and k norms
-        stream_after(sd, st, c->side_ev[2]);
-        gate16(c, mode, w->g2, b.attn_in, T, (float*)b.glog2, sd);
-        LtxEncArgs ea{ctxv, (const float*)w->psst.p, pts2, b.enc, S, sat};
-        c->launch(mode == LTX_MODE_BF16 ? "ltx_enc_bf16" : "ltx_enc_f16", S, 1, 1, 256, &ea, st);
-        g = LtxGemmArgs{};
-        g.out = b.k2_16;
-        g.out2 = b.vt2;
-        g.nsplit = LTX_D;
-        g.sat = sat;
-        g.part = (float*)b.part;  // split-K partial sums (small grids)
-        gemm16(c, mode, w->kv2, b.enc, S, LTX_D, LTX_EPI_QKV, g, st, "gemm:kv2");
-        qknorm16(c, mode, b.q2_16, LTX_D, w->qn2.p, nullptr, nullptr, b.qh2, T, kAttnC, st);
-        qknorm16(c, mode, b.k2_16, LTX_D, w->kn2.p, nullptr, nullptr, b.kh2, S, 1.0f, st);
-        stream_after(st, sd, c->side_ev[3]);  // glog2 ready
+        if (early) {
+            qknorm16(c, mode, b.q2_16, LTX_D, w->qn2.p, nullptr, nullptr, b.qh2, T, kAttnC, st);
+        } else {
+            // the cross-attention gate logits on the side stream, beside the
+            // context side (K/V modulation, k|v GEMM) and the q and k norms
+            stream_after(sd, st, c->side_ev[2]);
+            gate16(c, mode, w->g2, b.attn_in, T, (float*)b.glog2, sd);
+            ctx_side(st, b.part);
+            qknorm16(c, mode, b.q2_16, LTX_D, w->qn2.p, nullptr, nullptr, b.qh2, T, kAttnC, st);
+            qknorm16(c, mode, b.k2_16, LTX_D, w->kn2.p, nullptr, nullptr, b.kh2, S, 1.0f, st);
+        }
+        stream_after(st, sd, c->side_ev[3]);  // glog2 (and, early, the context side) ready
         attn16(c, mode, b.qh2, b.kh2, b.vt2, (const float*)b.glog2, b.o2, T, S, true, st, "attn:cross", sat, true);
     }
     g = LtxGemmArgs{};

@@ -103,7 +103,10 @@ struct ltx_ctx {
     // side stream of a forward: work off the main chain (gate logits, the
     // cross-attention K/V) overlaps it, ordered by the events
     hipStream_t side = nullptr;
-    hipEvent_t side_ev[4] = {};
+    hipEvent_t side_ev[5] = {};
+    // the small-T schedule of the side stream (block forward): 0 never, 1
+    // below kEarlySideRows tokens, 2 at every size (tests)
+    int side_early = 1;
     // markers recorded after each launch inside a MarkScope (see launch),
     // cycled; no timing, no system-scope fence
     hipEvent_t marks[16] = {};
@@ -150,6 +153,9 @@ struct MarkScope {
     MarkScope& operator=(const MarkScope&) = delete;
 };
 constexpr int kMarkRows = 8192;
+// below this many tokens the block's GEMM and attention grids leave CUs idle:
+// the side stream starts at the first RMSNorm + modulate (block_forward)
+constexpr int kEarlySideRows = 4096;
 
 void set_thread_error(const std::string& e);
 void block_forward(ltx_ctx* c, const ltx_block_weights* w, const float* x, const float* tstab, int K,

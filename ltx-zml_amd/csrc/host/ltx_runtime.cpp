@@ -183,13 +183,17 @@ int ltx_init(int device, ltx_ctx** out) {
         // GEMM nowhere / wherever the shape allows; LTX_GEMM_S4=off / all: the
         // small-grid GEMM likewise; LTX_ATTN_VARIANT=w8: the any-length attention
         // everywhere, =pp: the streaming ping-pong attention also for 64-256
-        // keys (the kernels each test exercises beside the defaults)
+        // keys; LTX_SIDE_EARLY=off / all: the small-T side-stream schedule
+        // of the block forward nowhere / at every size (the kernels and
+        // schedules each test exercises beside the defaults)
         if (const char* e = std::getenv("LTX_GEMM_GRID")) c->gemm_persistent = std::strcmp(e, "tile") != 0;
         if (const char* e = std::getenv("LTX_GEMM_Q8")) c->gemm_dma = std::strcmp(e, "reg") != 0;
         if (const char* e = std::getenv("LTX_GEMM_X4"))
             c->gemm_x4 = std::strcmp(e, "off") == 0 ? 0 : std::strcmp(e, "all") == 0 ? 2 : 1;
         if (const char* e = std::getenv("LTX_GEMM_S4"))
             c->gemm_s4 = std::strcmp(e, "off") == 0 ? 0 : std::strcmp(e, "all") == 0 ? 2 : 1;
+        if (const char* e = std::getenv("LTX_SIDE_EARLY"))
+            c->side_early = std::strcmp(e, "off") == 0 ? 0 : std::strcmp(e, "all") == 0 ? 2 : 1;
         if (const char* e = std::getenv("LTX_ATTN_VARIANT")) {
             c->attn_pp = std::strcmp(e, "w8") != 0;
             c->attn_kv = c->attn_pp && std::strcmp(e, "pp") != 0;

@@ -170,13 +170,17 @@ GEMM_VARIANTS = {
     # unquantised ones included, split over K where even its tiles fill at
     # most half the CUs
     "s4all": ("LTX_GEMM_S4", "all"),
+    # not a GEMM path: the large-T schedule of the side stream (gate logits
+    # after the q|k|v GEMM, the context side on the main stream) at these
+    # sizes, where the side stream otherwise starts at the first RMSNorm
+    "sideoff": ("LTX_SIDE_EARLY", "off"),
 }
 
 
 @pytest.fixture(scope="module", params=sorted(GEMM_VARIANTS))
 def ctx_gemm(request):
-    """A context with one GEMM path forced by its environment setting (read
-    when the context is made)."""
+    """A context with one GEMM path (or side-stream schedule) forced by its
+    environment setting (read when the context is made)."""
     import os
     var, val = GEMM_VARIANTS[request.param]
     old = os.environ.get(var)
