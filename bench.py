@@ -33,7 +33,7 @@ PEAK_F32_TFLOPS = 157.3  # MI355X fp32 (the f32 mode's kernels are SIMT f32)
 # FETCH_SIZE x 2.0 (the factor a 1 GiB copy calibrates) + WRITE_SIZE x 1.0,
 # measured on this kernel (profiles/block_t28672_hbm_bytes.md); None for a
 # size or type not profiled.
-ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.475e9, (28672, "bf16"): 2.470e9}
+ATTN_SELF_TRAFFIC = {(28672, "f16"): 2.467e9, (28672, "bf16"): 2.470e9}
 
 
 def flops(T: int, S: int) -> dict:
