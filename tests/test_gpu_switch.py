@@ -4,11 +4,12 @@ the W8A16 / small-grid kernels (split over K where their tiles fill at most
 half the CUs) and the second stream starts at the first RMSNorm with the
 whole context side; from 4,096 tokens the int8 weights are dequantised once
 and run the four-wave 16-bit GEMM (here with a 4-row last M-tile), and the
-second stream takes only the gate logits. 48 output rows (with the last
-tokens) and the three residual branches of those rows against the f64
-row-subset oracle, every projection int8 (the session's block with f32
-scales), fp16 operands: gate rel-RMS 2e-3 (the reference's per-block
-gate)."""
+second stream takes only the gate logits. T = 8,200 adds the launch markers
+that a forward records from 8,192 tokens (an 8-row last M-tile). 48 output
+rows (with the last tokens) and the three residual branches of those rows
+against the f64 row-subset oracle, every projection int8 (the session's
+block with f32 scales), fp16 operands: gate rel-RMS 2e-3 (the reference's
+per-block gate)."""
 import numpy as np
 import pytest
 
@@ -33,10 +34,10 @@ def _stage(ctx, name, T, rows):
     return t[torch.from_numpy(rows).cuda()].cpu().numpy().astype(np.float64)
 
 
-@pytest.mark.parametrize("T", [4095, 4100])
+@pytest.mark.parametrize("T", [4095, 4100, 8200])
 def test_block_rows_at_size_switch(ctx, block0_out, T):
     block_q8 = block0_out
-    say(f"block rows at the 4,096-token switch T={T} S={S}")
+    say(f"block rows at the size switches T={T} S={S}")
     inp = synth.make_inputs(T, S, sigma=0.7)
     cos, sin = rt.rope_tables(inp["grid"])
     rows = np.unique(np.concatenate([np.linspace(0, T - 1, 44).astype(np.int64), [1, T - 4, T - 3, T - 2]]))
