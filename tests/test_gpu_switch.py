@@ -9,7 +9,8 @@ that a forward records from 8,192 tokens (an 8-row last M-tile). 48 output
 rows (with the last tokens) and the three residual branches of those rows
 against the f64 row-subset oracle, every projection int8 (the session's
 block with f32 scales), fp16 operands: gate rel-RMS 2e-3 (the reference's
-per-block gate)."""
+per-block gate); bf16 operands at 4,100 tokens: the output 2e-3, its
+branches 1.5e-2 (as at the full size)."""
 import numpy as np
 import pytest
 
@@ -34,17 +35,17 @@ def _stage(ctx, name, T, rows):
     return t[torch.from_numpy(rows).cuda()].cpu().numpy().astype(np.float64)
 
 
-@pytest.mark.parametrize("T", [4095, 4100, 8200])
-def test_block_rows_at_size_switch(ctx, block0_out, T):
+@pytest.mark.parametrize("T,mode", [(4095, "f16"), (4100, "f16"), (8200, "f16"), (4100, "bf16")])
+def test_block_rows_at_size_switch(ctx, block0_out, T, mode):
     block_q8 = block0_out
-    say(f"block rows at the size switches T={T} S={S}")
+    say(f"block rows at the size switches T={T} S={S} mode={mode}")
     inp = synth.make_inputs(T, S, sigma=0.7)
     cos, sin = rt.rope_tables(inp["grid"])
     rows = np.unique(np.concatenate([np.linspace(0, T - 1, 44).astype(np.int64), [1, T - 4, T - 3, T - 2]]))
     w = ctx.upload(block_q8)
     y = torch.empty((T, 4096), dtype=torch.float32, device="cuda")
     ctx.forward(w, dev(inp["x"]), dev(inp["tstab"]), dev(inp["tidx"]), dev(inp["ctx"]), dev(inp["pts2"]), dev(cos),
-                dev(sin), y, mode=rt.MODE_F16)
+                dev(sin), y, mode=rt.MODES[mode])
     torch.cuda.synchronize()
     assert torch.isfinite(y).all().item()
     got = y[torch.from_numpy(rows).cuda()].cpu().numpy().astype(np.float64)
@@ -58,4 +59,5 @@ def test_block_rows_at_size_switch(ctx, block0_out, T):
          "ca_branch": oracle.rel_rms(x_ca - x_sa, wst["s5_ca_out"]),
          "ff_branch": oracle.rel_rms(got - x_ca, want - wst["x_ca"])}
     say("  " + " ".join(f"{k}={v:.2e}" for k, v in r.items()))
-    assert all(v <= 2e-3 for v in r.values()), r
+    assert r["y"] <= 2e-3, r
+    assert all(v <= (2e-3 if mode == "f16" else 1.5e-2) for v in r.values()), r
